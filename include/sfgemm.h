@@ -1,0 +1,213 @@
+/*
+ * sfgemm.h — C ABI of the MI355X (gfx950) matmul hot path.
+ *
+ * Plain C: only <stdint.h>/<stddef.h>, no HIP or CUDA headers, so the
+ * Cython seam (scaffolding_amd/_cuda_ops.pyx) and any other FFI (ctypes,
+ * cffi) bind it with a C compiler.  Streams and events are opaque
+ * pointers; NULL means the device's default stream.
+ *
+ * Every function returns an int status: 0 on success, a negative SF_ERR_*
+ * code otherwise.  Nothing here prints.  sf_status_string() maps a code to
+ * text and sf_last_error() returns the detail of the most recent failure on
+ * the calling thread.
+ *
+ * All matrices are row-major.  Problem sizes and leading dimensions count
+ * ELEMENTS, never bytes.
+ *
+ * Reference interface this replaces (all /root/reference paths):
+ *   _cuda_ops_decl.h:107-117   cuda_sgemm / cuda_sgemm_batched (cuBLAS)
+ *   _cuda_ops_decl.h:136-137   cuda_bias_add_row_f32
+ *   _cuda_ops_decl.h:63-72     cuda_silu_f32 / cuda_gelu_f32
+ *   _cuda_ops_decl.h:59        cuda_muls_f32
+ *   _cuda_ops_decl.h:78-79     cuda_softmax_f32
+ *   _cuda_ops.pyx:33-142       CUDA runtime calls the Cython module binds
+ *                              directly (malloc/free/memcpy/device/stream/event)
+ *   _cuda_ops.pyx:357-475      caching allocator (here native, in C++)
+ */
+#ifndef SFGEMM_H
+#define SFGEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ */
+/* Types and status codes                                              */
+/* ------------------------------------------------------------------ */
+
+typedef enum {
+    SF_F32 = 0,   /* IEEE binary32                                  */
+    SF_F16 = 1,   /* IEEE binary16                                  */
+    SF_BF16 = 2   /* bfloat16 (upper half of binary32), stored u16  */
+} sf_dtype;
+
+/* Epilogue applied to v = alpha * (op(A) . op(B)) in fp32 registers before
+ * the single rounding to the output dtype:
+ *   NONE            y = v
+ *   BIAS            y = v + bias[n]
+ *   BIAS_SILU       y = silu(v + bias[n])       silu(t) = t / (1 + e^-t)
+ *   BIAS_GELU_TANH  y = gelu_tanh(v + bias[n])
+ *   SILU            y = silu(v)
+ *   GELU_TANH       y = gelu_tanh(v)
+ * gelu_tanh(t) = 0.5 t (1 + tanh(0.7978845608 (t + 0.044715 t^3))). */
+typedef enum {
+    SF_EPI_NONE = 0,
+    SF_EPI_BIAS = 1,
+    SF_EPI_BIAS_SILU = 2,
+    SF_EPI_BIAS_GELU_TANH = 3,
+    SF_EPI_SILU = 4,
+    SF_EPI_GELU_TANH = 5
+} sf_epilogue;
+
+#define SF_OK 0
+#define SF_ERR_HIP (-1)          /* a HIP runtime call failed              */
+#define SF_ERR_INVALID_ARG (-2)  /* bad size, stride, pointer or enum      */
+#define SF_ERR_UNSUPPORTED (-3)  /* valid request this library does not do */
+#define SF_ERR_NO_DEVICE (-4)    /* no usable GPU                          */
+#define SF_ERR_OOM (-5)          /* device allocation failed               */
+
+const char* sf_status_string(int status);
+/* Detail text of the last failing call on this thread ("" if none). */
+const char* sf_last_error(void);
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+int sf_version(void);
+
+/* ------------------------------------------------------------------ */
+/* GEMM family                                                         */
+/* ------------------------------------------------------------------ */
+
+/* C[b] = epi(alpha * op(A[b]) . op(B[b]) (+ bias)) for b in [0, batch).
+ *
+ * Replaces cuda_sgemm (_cuda_kernels.cu:1175-1220, decl
+ * _cuda_ops_decl.h:107-111), cuda_sgemm_batched (_cuda_kernels.cu:1223-1243,
+ * decl _cuda_ops_decl.h:112-117) and the separate passes
+ * cuda_bias_add_row_f32 (_cuda_kernels.cu:1490-1527), cuda_silu_f32 /
+ * cuda_gelu_f32 (_cuda_kernels.cu:384,428) and cuda_muls_f32
+ * (_cuda_kernels.cu:237-277), which it fuses into the epilogue.
+ *
+ *   op(A) is M x K: A is stored M x K (lda >= K) when transA == 0.
+ *   op(B) is K x N: B is stored K x N (ldb >= N) when transB == 0, or
+ *                   N x K (ldb >= K) when transB != 0 ("NT", x . W^T).
+ *   C is M x N, ldc >= N.
+ *   strideA/B/C: element offset between consecutive batch entries;
+ *   strideA or strideB 0 broadcasts that operand over the batch (this is
+ *   np.matmul's rule for a 2-D operand); strideC must be >= M*ldc when
+ *   batch > 1.
+ *
+ * Dtypes: ab_dtype in {F32, F16, BF16} for both A and B.  c_dtype is
+ * ab_dtype or F32.  bias (length N, NULL unless the epilogue has BIAS) has
+ * dtype ab_dtype.  F32 inputs run on fp32 MFMA (v_mfma_f32_16x16x4_f32);
+ * F16/BF16 inputs on 16-bit MFMA with fp32 accumulation.
+ *
+ * transA != 0 returns SF_ERR_UNSUPPORTED (no caller on the path uses it).
+ * M, N or batch == 0 is a no-op; K == 0 writes epi(0 (+ bias)).
+ * The call is asynchronous on `stream`. */
+int sf_gemm(int transA, int transB,
+            int64_t M, int64_t N, int64_t K, int64_t batch,
+            const void* A, int64_t lda, int64_t strideA,
+            const void* B, int64_t ldb, int64_t strideB,
+            void* C, int64_t ldc, int64_t strideC,
+            sf_dtype ab_dtype, sf_dtype c_dtype, float alpha,
+            const void* bias, sf_epilogue epi, void* stream);
+
+/* Diagnostic twin of sf_gemm: validates the same arguments and writes the
+ * name of the kernel sf_gemm would launch (e.g. "gemm tile 256x256",
+ * "gemm skinny") into buf[len] without launching anything.  Host-only, no
+ * reference counterpart (cuBLAS chooses its kernels internally). */
+int sf_gemm_plan(int transA, int transB,
+                 int64_t M, int64_t N, int64_t K, int64_t batch,
+                 const void* A, int64_t lda, int64_t strideA,
+                 const void* B, int64_t ldb, int64_t strideB,
+                 void* C, int64_t ldc, int64_t strideC,
+                 sf_dtype ab_dtype, sf_dtype c_dtype, float alpha,
+                 const void* bias, sf_epilogue epi, char* buf, int len);
+
+/* Row softmax: y[r,:] = softmax(scale * x[r,:]) for r in [0, rows).
+ * Contiguous rows of `cols` elements.  Replaces cuda_softmax_f32
+ * (_cuda_kernels.cu:473-640, decl _cuda_ops_decl.h:78-79) with the
+ * dev_muls pre-scale of scaled_dot_product_attention
+ * (nn/functional.py:315-316) folded in.  in/out dtypes independently
+ * F32/F16/BF16; arithmetic is fp32. */
+int sf_softmax_rows(const void* x, void* y, int64_t rows, int64_t cols,
+                    sf_dtype in_dtype, sf_dtype out_dtype, float scale,
+                    void* stream);
+
+/* Standalone elementwise ops over n contiguous elements of dtype `dt`
+ * (arithmetic in fp32, one rounding on store).  x == y is allowed.
+ *   sf_silu  replaces cuda_silu_f32 (_cuda_kernels.cu:384)
+ *   sf_gelu  replaces cuda_gelu_f32 (_cuda_kernels.cu:428), tanh form
+ *   sf_muls  replaces cuda_muls_f32 (_cuda_kernels.cu:237-277)          */
+int sf_silu(const void* x, void* y, int64_t n, sf_dtype dt, void* stream);
+int sf_gelu(const void* x, void* y, int64_t n, sf_dtype dt, void* stream);
+int sf_muls(const void* x, float s, void* y, int64_t n, sf_dtype dt,
+            void* stream);
+
+/* C[i,j] += bias[j] in place on a contiguous M x N matrix.
+ * Replaces cuda_bias_add_row_f32 (_cuda_kernels.cu:1490-1527,
+ * decl _cuda_ops_decl.h:136-137). */
+int sf_bias_add_rows(void* C, const void* bias, int64_t M, int64_t N,
+                     sf_dtype dt, void* stream);
+
+/* Dtype conversion of n contiguous elements (RNE; NaN stays NaN, +-Inf
+ * and signed zero are preserved).  Has no reference counterpart: the
+ * reference stores bfloat16 as float32 (dtype.py:31); this library keeps
+ * real 16-bit storage and converts on the device. */
+int sf_cast(const void* x, sf_dtype in_dtype, void* y, sf_dtype out_dtype,
+            int64_t n, void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Runtime: devices, memory, streams, events                           */
+/* (the CUDA runtime calls _cuda_ops.pyx:33-142 binds directly)        */
+/* ------------------------------------------------------------------ */
+
+int sf_get_device_count(int* count);
+int sf_set_device(int device);
+int sf_get_device(int* device);
+int sf_device_synchronize(void);
+/* name: NUL-terminated into buf[len]; arch: e.g. "gfx950". */
+int sf_get_device_name(int device, char* buf, int len);
+int sf_get_device_arch(int device, char* buf, int len);
+int sf_get_device_props(int device, int* cu_count, int64_t* total_mem,
+                        int* clock_khz, int* l2_bytes);
+int sf_mem_get_info(size_t* free_bytes, size_t* total_bytes);
+
+/* Raw allocation (hipMalloc / hipFree) on the current device. */
+int sf_malloc(void** ptr, size_t nbytes);
+int sf_free(void* ptr);
+
+/* Caching allocator (replaces _cuda_ops.pyx:357-475): per-device pools
+ * keyed by exact size rounded up to 256 bytes, capped per device (bytes
+ * beyond the cap go back to hipFree).  sf_cache_alloc switches to
+ * `device` for the allocation and restores the caller's device. */
+int sf_cache_alloc(int device, size_t nbytes, void** ptr, size_t* got_bytes);
+int sf_cache_free(int device, void* ptr, size_t nbytes);
+int sf_cache_empty(int device);          /* device < 0: every device */
+int sf_cache_stats(int device, size_t* pooled_bytes, size_t* live_bytes);
+int sf_cache_set_limit(size_t bytes_per_device);
+
+/* Copies; synchronous w.r.t. the host when stream is NULL. */
+int sf_memcpy_h2d(void* dst, const void* src, size_t nbytes, void* stream);
+int sf_memcpy_d2h(void* dst, const void* src, size_t nbytes, void* stream);
+int sf_memcpy_d2d(void* dst, const void* src, size_t nbytes, void* stream);
+/* Fill nbytes with zero using a kernel (never a memset node). */
+int sf_zero(void* dst, size_t nbytes, void* stream);
+
+int sf_stream_create(void** stream);     /* default priority, non-blocking */
+int sf_stream_destroy(void* stream);
+int sf_stream_synchronize(void* stream);
+
+int sf_event_create(void** event);
+int sf_event_destroy(void* event);
+int sf_event_record(void* event, void* stream);
+int sf_event_synchronize(void* event);
+int sf_stream_wait_event(void* stream, void* event);
+int sf_event_elapsed_ms(float* ms, void* start, void* end);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* SFGEMM_H */

@@ -1,0 +1,132 @@
+"""The reference's Linux CPU path for the matmul hot path, restated in NumPy
+(test infrastructure; never imported by the product path).
+
+On Linux the reference computes every operation of this path with NumPy
+(its Cython CPU kernels are built on macOS only, reference setup.py:319-333),
+so the restatement below is the same sequence of NumPy calls:
+
+  matmul        np.matmul(a, b)                       reference tensor.py:1516-1519
+  matmul_nt     matmul(a, b.transpose(-2, -1))        reference tensor.py:1538-1539
+  linear        x @ W.T (+ b)                         reference nn/layers.py:129-131
+  F.linear      np.matmul(x, W.T) (+ b)               reference nn/functional.py:388-393
+  silu          x * (1 / (1 + exp(-x)))               reference nn/functional.py:58-59
+  gelu (tanh)   0.5 x (1 + tanh(sqrt(2/pi)(x + 0.044715 x^3)))
+                                                      reference nn/functional.py:79-82
+  softmax       e = exp(x - max); e / sum(e)          reference nn/functional.py:137-141
+  sdpa          scores = q @ k^T; *= scale; softmax; @ v
+                                                      reference nn/functional.py:323-357
+
+The *_f64 functions are the closed forms in float64 on the (already
+quantized) inputs: the accuracy oracle for every dtype.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+SQRT_2_OVER_PI = math.sqrt(2.0 / math.pi)
+GELU_C = 0.044715
+
+
+# ---------------------------------------------------------------- fp32 path
+
+def matmul(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """reference tensor.py:1516-1519 (Linux CPU branch)."""
+    return np.matmul(a, b)
+
+
+def matmul_nt(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """reference tensor.py:1538-1539: matmul(a, b.transpose(-2, -1))."""
+    return np.matmul(a, np.swapaxes(b, -2, -1))
+
+
+def linear(x: np.ndarray, w: np.ndarray, b: np.ndarray | None = None) -> np.ndarray:
+    """reference nn/layers.py:129-131: result = x @ W.T; result + bias."""
+    y = x @ w.T
+    if b is not None:
+        y = y + b
+    return y
+
+
+def silu(x: np.ndarray) -> np.ndarray:
+    """reference nn/functional.py:58-59."""
+    sig = 1.0 / (1.0 + np.exp(-x))
+    return x * sig
+
+
+def gelu_tanh(x: np.ndarray) -> np.ndarray:
+    """reference nn/functional.py:79-82."""
+    return 0.5 * x * (1 + np.tanh(SQRT_2_OVER_PI * (x + GELU_C * x ** 3)))
+
+
+def softmax(x: np.ndarray, axis: int = -1) -> np.ndarray:
+    """reference nn/functional.py:137-141."""
+    x_max = x.max(axis=axis, keepdims=True)
+    e = np.exp(x - x_max)
+    e_sum = e.sum(axis=axis, keepdims=True)
+    np.divide(e, e_sum, out=e)
+    return e
+
+
+def sdpa(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float | None = None) -> np.ndarray:
+    """reference nn/functional.py:323-357 without mask and dropout."""
+    d = q.shape[-1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    scores = np.matmul(q, np.swapaxes(k, -2, -1))
+    scores *= scale
+    s_max = scores.max(axis=-1, keepdims=True)
+    scores -= s_max
+    np.exp(scores, out=scores)
+    s_sum = scores.sum(axis=-1, keepdims=True)
+    np.divide(scores, s_sum, out=scores)
+    return np.matmul(scores, v)
+
+
+# ------------------------------------------------------- fp64 closed forms
+
+def act_f64(y: np.ndarray, act: str | None) -> np.ndarray:
+    if act in (None, "none"):
+        return y
+    if act == "silu":
+        return y / (1.0 + np.exp(-y))
+    if act in ("gelu", "gelu_tanh"):
+        return 0.5 * y * (1.0 + np.tanh(SQRT_2_OVER_PI * (y + GELU_C * y ** 3)))
+    raise ValueError(act)
+
+
+def linear_f64(x, w, b=None, act: str | None = None, alpha: float = 1.0) -> np.ndarray:
+    """act(alpha * x . W^T + b) in float64."""
+    y = alpha * (np.asarray(x, np.float64) @ np.asarray(w, np.float64).T)
+    if b is not None:
+        y = y + np.asarray(b, np.float64)
+    return act_f64(y, act)
+
+
+def matmul_f64(a, b) -> np.ndarray:
+    return np.matmul(np.asarray(a, np.float64), np.asarray(b, np.float64))
+
+
+def softmax_f64(x, scale: float = 1.0) -> np.ndarray:
+    s = np.asarray(x, np.float64) * scale
+    s = s - s.max(axis=-1, keepdims=True)
+    e = np.exp(s)
+    return e / e.sum(axis=-1, keepdims=True)
+
+
+def sdpa_f64(q, k, v, scale: float) -> np.ndarray:
+    s = np.matmul(np.asarray(q, np.float64), np.swapaxes(np.asarray(k, np.float64), -2, -1))
+    return np.matmul(softmax_f64(s, scale), np.asarray(v, np.float64))
+
+
+# ------------------------------------------------------------ brute force
+
+def matmul_bruteforce(a, b) -> list:
+    """Triple loop in Python floats (fp64) for tiny 2-D inputs: the
+    index-by-index definition C[i][j] = sum_k A[i][k] B[k][j]."""
+    m, k = len(a), len(a[0])
+    n = len(b[0])
+    assert len(b) == k
+    return [[math.fsum(float(a[i][p]) * float(b[p][j]) for p in range(k)) for j in range(n)]
+            for i in range(m)]

@@ -1,0 +1,788 @@
+# cython: language_level=3, cdivision=True
+"""
+_cuda_ops — the operator seam of the matmul hot path, MI355X edition.
+
+Exports the Python names Scaffolding's tensor / nn layers import as
+``_cuops`` (reference seam: /root/reference/_cuda_ops.pyx; importers listed
+at tensor.py:36-41, nn/layers.py:12, nn/functional.py:11).  Every compute
+entry point calls libsfgemm's C ABI (include/sfgemm.h) on the HIP device;
+nothing here computes on the host.  There is no fallback: without the
+library this module does not import, and without a GPU every device call
+raises RuntimeError.
+
+Differences from the reference, on purpose:
+  * real 16-bit storage: GpuTensor.dtype may be np.float16 or BFLOAT16 (a
+    2-byte structured dtype standing for bfloat16); GEMM outputs keep the
+    input dtype, as np.matmul does, instead of always being tagged fp32
+    (reference _cuda_ops.pyx:1102,1149,1302);
+  * dev_linear_forward takes an optional fused activation ('silu' or
+    'gelu'), and dev_batched_matmul_nt / dev_matmul_nt an alpha, so bias,
+    activation and the SDPA scale are GEMM epilogues, not extra passes;
+  * batched matmul broadcasts a 2-D operand over the other's batch, as
+    np.matmul does (the reference assumes equal batch, :1122-1149);
+  * dev_softmax over a non-last dim raises instead of silently using the
+    last dim (reference :1016-1034 ignores `dim`).
+"""
+
+import numpy as np
+cimport numpy as cnp
+from libc.stdint cimport int64_t, uintptr_t
+from libc.string cimport memset
+
+cnp.import_array()
+
+cdef extern from "sfgemm.h" nogil:
+    ctypedef enum sf_dtype:
+        SF_F32
+        SF_F16
+        SF_BF16
+    ctypedef enum sf_epilogue:
+        SF_EPI_NONE
+        SF_EPI_BIAS
+        SF_EPI_BIAS_SILU
+        SF_EPI_BIAS_GELU_TANH
+        SF_EPI_SILU
+        SF_EPI_GELU_TANH
+    int SF_OK
+    int SF_ERR_HIP
+    int SF_ERR_INVALID_ARG
+    int SF_ERR_UNSUPPORTED
+    int SF_ERR_NO_DEVICE
+    int SF_ERR_OOM
+
+    const char* sf_status_string(int status)
+    const char* sf_last_error()
+    int sf_version()
+
+    int sf_gemm(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t batch,
+                const void* A, int64_t lda, int64_t strideA,
+                const void* B, int64_t ldb, int64_t strideB,
+                void* C, int64_t ldc, int64_t strideC,
+                sf_dtype ab_dtype, sf_dtype c_dtype, float alpha,
+                const void* bias, sf_epilogue epi, void* stream)
+    int sf_gemm_plan(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t batch,
+                     const void* A, int64_t lda, int64_t strideA,
+                     const void* B, int64_t ldb, int64_t strideB,
+                     void* C, int64_t ldc, int64_t strideC,
+                     sf_dtype ab_dtype, sf_dtype c_dtype, float alpha,
+                     const void* bias, sf_epilogue epi, char* buf, int len)
+    int sf_softmax_rows(const void* x, void* y, int64_t rows, int64_t cols,
+                        sf_dtype in_dtype, sf_dtype out_dtype, float scale, void* stream)
+    int sf_silu(const void* x, void* y, int64_t n, sf_dtype dt, void* stream)
+    int sf_gelu(const void* x, void* y, int64_t n, sf_dtype dt, void* stream)
+    int sf_muls(const void* x, float s, void* y, int64_t n, sf_dtype dt, void* stream)
+    int sf_bias_add_rows(void* C, const void* bias, int64_t M, int64_t N, sf_dtype dt, void* stream)
+    int sf_cast(const void* x, sf_dtype in_dtype, void* y, sf_dtype out_dtype, int64_t n, void* stream)
+
+    int sf_get_device_count(int* count)
+    int sf_set_device(int device)
+    int sf_get_device(int* device)
+    int sf_device_synchronize()
+    int sf_get_device_name(int device, char* buf, int len)
+    int sf_get_device_arch(int device, char* buf, int len)
+    int sf_get_device_props(int device, int* cu_count, int64_t* total_mem, int* clock_khz, int* l2_bytes)
+    int sf_mem_get_info(size_t* free_bytes, size_t* total_bytes)
+    int sf_cache_alloc(int device, size_t nbytes, void** ptr, size_t* got_bytes)
+    int sf_cache_free(int device, void* ptr, size_t nbytes)
+    int sf_cache_empty(int device)
+    int sf_cache_stats(int device, size_t* pooled_bytes, size_t* live_bytes)
+    int sf_cache_set_limit(size_t bytes_per_device)
+    int sf_memcpy_h2d(void* dst, const void* src, size_t nbytes, void* stream)
+    int sf_memcpy_d2h(void* dst, const void* src, size_t nbytes, void* stream)
+    int sf_memcpy_d2d(void* dst, const void* src, size_t nbytes, void* stream)
+    int sf_zero(void* dst, size_t nbytes, void* stream)
+    int sf_stream_create(void** stream)
+    int sf_stream_destroy(void* stream)
+    int sf_stream_synchronize(void* stream)
+    int sf_event_create(void** event)
+    int sf_event_destroy(void* event)
+    int sf_event_record(void* event, void* stream)
+    int sf_event_synchronize(void* event)
+    int sf_stream_wait_event(void* stream, void* event)
+    int sf_event_elapsed_ms(float* ms, void* start, void* end)
+
+
+# ================================================================
+#  dtypes
+# ================================================================
+
+# bfloat16 storage dtype: 2 bytes, distinct from np.uint16 so it can never
+# be mistaken for integer data.  Host views of device bfloat16 data are
+# widened to float32 (the reference's own host mapping, dtype.py:31).
+BFLOAT16 = np.dtype([('bf16', '<u2')])
+
+_F32 = np.dtype(np.float32)
+_F16 = np.dtype(np.float16)
+
+
+cdef sf_dtype _sf_dtype(object dt) except *:
+    d = np.dtype(dt) if not isinstance(dt, np.dtype) else dt
+    if d == _F32:
+        return SF_F32
+    if d == _F16:
+        return SF_F16
+    if d == BFLOAT16:
+        return SF_BF16
+    raise TypeError("unsupported device dtype %r (float32, float16, bfloat16 only)" % (dt,))
+
+
+cdef size_t _itemsize(object dt) except 0:
+    return (<object>np.dtype(dt)).itemsize
+
+
+def resolve_dtype(dt):
+    """Maps 'bfloat16' / 'float16' / 'float32' / numpy dtypes to the device
+    storage dtype used in GpuTensor.dtype."""
+    if isinstance(dt, str):
+        if dt in ('bfloat16', 'bf16'):
+            return BFLOAT16
+        return np.dtype(dt)
+    if isinstance(dt, np.dtype):
+        return dt
+    return np.dtype(dt)
+
+
+# ================================================================
+#  Errors (text as the reference's _cuda_ops.pyx:292-300)
+# ================================================================
+
+cdef inline str _detail(int ret):
+    cdef const char* d = sf_last_error()
+    msg = d.decode('utf-8', 'replace') if d != NULL else ''
+    if not msg:
+        msg = sf_status_string(ret).decode('utf-8')
+    return msg
+
+
+cdef inline void _check_cuda(int ret) except *:
+    if ret != SF_OK:
+        raise RuntimeError("CUDA error: %s" % _detail(ret))
+
+
+cdef inline void _check_kernel(int ret) except *:
+    if ret != SF_OK:
+        raise RuntimeError("CUDA kernel launch failed with ret code %d: %s" % (ret, _detail(ret)))
+
+
+# ================================================================
+#  Device buffer (reference CudaBuffer, _cuda_ops.pyx:307-341)
+# ================================================================
+
+cdef class CudaBuffer:
+    """Owning handle of device memory from the native caching allocator;
+    returned to the pool when the Python object dies."""
+    cdef void* ptr
+    cdef size_t nbytes
+    cdef int device_id
+    cdef bint owns_memory
+
+    def __cinit__(self):
+        self.ptr = NULL
+        self.nbytes = 0
+        self.device_id = 0
+        self.owns_memory = False
+
+    def __dealloc__(self):
+        if self.owns_memory and self.ptr != NULL:
+            sf_cache_free(self.device_id, self.ptr, self.nbytes)
+            self.ptr = NULL
+
+    @property
+    def data_ptr(self):
+        return <uintptr_t>self.ptr
+
+    @property
+    def size(self):
+        return self.nbytes
+
+    @property
+    def device(self):
+        return self.device_id
+
+
+cdef CudaBuffer _make_buffer(size_t nbytes, int device_id):
+    cdef CudaBuffer buf = CudaBuffer.__new__(CudaBuffer)
+    cdef size_t got = 0
+    cdef void* p = NULL
+    cdef int ret
+    with nogil:
+        ret = sf_cache_alloc(device_id, nbytes, &p, &got)
+    _check_cuda(ret)
+    buf.ptr = p
+    buf.nbytes = got
+    buf.device_id = device_id
+    buf.owns_memory = True
+    return buf
+
+
+cdef int _current_device() except -1:
+    cdef int dev = 0
+    _check_cuda(sf_get_device(&dev))
+    return dev
+
+
+def empty_cache(int device=-1):
+    """Frees every pooled (unused) device block (reference :413-437)."""
+    _check_cuda(sf_cache_empty(device))
+
+
+def cache_stats(int device=-1):
+    """(pooled_bytes, live_bytes) of the native caching allocator."""
+    cdef size_t pooled = 0, live = 0
+    sf_cache_stats(device, &pooled, &live)
+    return int(pooled), int(live)
+
+
+def set_cache_limit(size_t nbytes):
+    sf_cache_set_limit(nbytes)
+
+
+# ================================================================
+#  GpuTensor (reference _cuda_ops.pyx:807-819)
+# ================================================================
+
+class GpuTensor:
+    """GPU-resident, C-contiguous tensor: a CudaBuffer plus shape and dtype."""
+    __slots__ = ('buffer', 'shape', 'dtype', 'numel', 'device_id')
+
+    def __init__(self, buffer, tuple shape, dtype, int device_id=-1):
+        self.buffer = buffer
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = resolve_dtype(dtype)
+        self.device_id = device_id if device_id >= 0 else (<CudaBuffer>buffer).device_id
+        cdef int64_t n = 1
+        for s in self.shape:
+            n *= s
+        self.numel = n
+
+    @property
+    def nbytes(self):
+        return self.numel * self.dtype.itemsize
+
+    @property
+    def data_ptr(self):
+        return (<CudaBuffer>self.buffer).data_ptr
+
+    def __repr__(self):
+        name = 'bfloat16' if self.dtype == BFLOAT16 else str(self.dtype)
+        return "GpuTensor(shape=%s, dtype=%s, device=%d)" % (self.shape, name, self.device_id)
+
+
+cdef inline void* _ptr(gt) except? NULL:
+    return (<CudaBuffer>(gt.buffer)).ptr
+
+
+cdef object _alloc_like(tuple shape, dtype, int device_id):
+    cdef int64_t n = 1
+    for s in shape:
+        n *= s
+    cdef size_t nbytes = <size_t>n * _itemsize(dtype)
+    return GpuTensor(_make_buffer(nbytes, device_id), shape, dtype, device_id)
+
+
+def empty(tuple shape, dtype=np.float32, int device_id=-1):
+    """Uninitialised device tensor."""
+    if device_id < 0:
+        device_id = _current_device()
+    return _alloc_like(shape, resolve_dtype(dtype), device_id)
+
+
+def zeros(tuple shape, dtype=np.float32, int device_id=-1):
+    gt = empty(shape, dtype, device_id)
+    cdef size_t nb = gt.nbytes
+    _check_kernel(sf_zero(_ptr(gt), nb, NULL))
+    return gt
+
+
+def gputensor_from_numpy(cnp.ndarray arr not None, int device_id=-1, dtype=None):
+    """Uploads a NumPy array (reference :822-840).  dtype='bfloat16' (or
+    BFLOAT16) uploads float32 data and rounds it to bfloat16 on the device
+    (RNE); dtype=np.float16 likewise from float32 input."""
+    cdef int target = device_id
+    cdef int prev = 0
+    if target < 0:
+        target = _current_device()
+    target_dt = resolve_dtype(dtype) if dtype is not None else arr.dtype
+    if target_dt == BFLOAT16 and arr.dtype == BFLOAT16:
+        src = np.ascontiguousarray(arr)
+        host_dt = BFLOAT16
+    elif target_dt == BFLOAT16 or (dtype is not None and target_dt != arr.dtype):
+        src = np.ascontiguousarray(arr, dtype=np.float32)
+        host_dt = _F32
+    else:
+        src = np.ascontiguousarray(arr)
+        host_dt = src.dtype
+    if host_dt != BFLOAT16 and host_dt not in (_F32, _F16):
+        raise TypeError("gputensor_from_numpy: unsupported dtype %r" % (arr.dtype,))
+    cdef cnp.ndarray flat = src.reshape(-1)
+    cdef size_t nbytes = flat.nbytes
+    shape = tuple((<object>arr).shape)
+    staged = _alloc_like(shape, host_dt, target)
+    _check_cuda(sf_get_device(&prev))
+    if prev != target:
+        _check_cuda(sf_set_device(target))
+    try:
+        _check_cuda(sf_memcpy_h2d(_ptr(staged), cnp.PyArray_DATA(flat), nbytes, NULL))
+        if host_dt == target_dt:
+            return staged
+        out = _alloc_like(shape, target_dt, target)
+        _check_kernel(sf_cast(_ptr(staged), _sf_dtype(host_dt), _ptr(out), _sf_dtype(target_dt),
+                              staged.numel, NULL))
+        return out
+    finally:
+        if prev != target:
+            sf_set_device(prev)
+
+
+def gputensor_to_numpy(gt):
+    """Downloads a GpuTensor (reference :843-858).  bfloat16 data comes back
+    widened to float32 (exact)."""
+    cdef int prev = 0
+    cdef int tgt = gt.device_id
+    cdef cnp.ndarray result
+    _check_cuda(sf_get_device(&prev))
+    if prev != tgt:
+        _check_cuda(sf_set_device(tgt))
+    try:
+        src = gt
+        if gt.dtype == BFLOAT16:
+            src = _alloc_like(gt.shape, _F32, tgt)
+            _check_kernel(sf_cast(_ptr(gt), SF_BF16, _ptr(src), SF_F32, gt.numel, NULL))
+        result = np.empty(src.shape, dtype=src.dtype)
+        _check_cuda(sf_memcpy_d2h(cnp.PyArray_DATA(result), _ptr(src), <size_t>result.nbytes, NULL))
+        return result
+    finally:
+        if prev != tgt:
+            sf_set_device(prev)
+
+
+def gputensor_bits_to_numpy(gt):
+    """Raw storage download: bfloat16 as uint16 bit patterns."""
+    cdef cnp.ndarray result
+    dt = np.dtype(np.uint16) if gt.dtype == BFLOAT16 else gt.dtype
+    result = np.empty(gt.shape, dtype=dt)
+    _check_cuda(sf_memcpy_d2h(cnp.PyArray_DATA(result), _ptr(gt), <size_t>result.nbytes, NULL))
+    return result
+
+
+def gputensor_from_bits(cnp.ndarray bits not None, int device_id=-1):
+    """Uploads uint16 bfloat16 bit patterns as a bfloat16 GpuTensor."""
+    if bits.dtype != np.uint16:
+        raise TypeError("gputensor_from_bits expects uint16 bit patterns")
+    return gputensor_from_numpy(np.ascontiguousarray(bits).view(BFLOAT16), device_id)
+
+
+def gputensor_to_device(gt, int target_dev):
+    """Copies a GpuTensor to another device (reference :861-875)."""
+    if gt.device_id == target_dev:
+        return gt
+    out = _alloc_like(gt.shape, gt.dtype, target_dev)
+    _check_cuda(sf_memcpy_d2d(_ptr(out), _ptr(gt), <size_t>gt.nbytes, NULL))
+    _check_cuda(sf_device_synchronize())
+    return out
+
+
+def dev_cast(gt, dtype):
+    """Device dtype conversion (RNE)."""
+    dt = resolve_dtype(dtype)
+    if dt == gt.dtype:
+        return gt
+    out = _alloc_like(gt.shape, dt, gt.device_id)
+    _check_kernel(sf_cast(_ptr(gt), _sf_dtype(gt.dtype), _ptr(out), _sf_dtype(dt), gt.numel, NULL))
+    return out
+
+
+def dev_reshape(gt, tuple shape):
+    """Metadata-only view (reference :1397-1420)."""
+    cdef int64_t n = 1
+    for s in shape:
+        n *= s
+    if n != gt.numel:
+        raise ValueError("cannot reshape %s into %s" % (gt.shape, shape))
+    return GpuTensor(gt.buffer, shape, gt.dtype, gt.device_id)
+
+
+# ================================================================
+#  Devices, streams, events (reference :491-685)
+# ================================================================
+
+def get_device_count():
+    cdef int n = 0
+    if sf_get_device_count(&n) != SF_OK:
+        return 0
+    return n
+
+
+def set_device(int device):
+    _check_cuda(sf_set_device(device))
+
+
+def get_current_device():
+    return _current_device()
+
+
+def device_synchronize():
+    cdef int ret
+    with nogil:
+        ret = sf_device_synchronize()
+    _check_cuda(ret)
+
+
+def get_device_name(int device=0):
+    cdef char buf[256]
+    _check_cuda(sf_get_device_name(device, buf, 256))
+    return buf.decode('utf-8', 'replace')
+
+
+def get_device_arch(int device=0):
+    cdef char buf[256]
+    _check_cuda(sf_get_device_arch(device, buf, 256))
+    return buf.decode('utf-8', 'replace')
+
+
+def get_device_properties(int device):
+    cdef int cus = 0, clk = 0, l2 = 0
+    cdef int64_t mem = 0
+    _check_cuda(sf_get_device_props(device, &cus, &mem, &clk, &l2))
+    return {
+        'name': get_device_name(device),
+        'arch': get_device_arch(device),
+        'total_memory': int(mem),
+        'multi_processor_count': cus,
+        'clock_rate_khz': clk,
+        'l2_cache_size': l2,
+    }
+
+
+def get_device_capability(int device=0):
+    """(9, 5) for gfx950."""
+    arch = get_device_arch(device).split(':')[0]
+    digits = arch[3:] if arch.startswith('gfx') else ''
+    if len(digits) >= 3:
+        return (int(digits[:-2]), int(digits[-2:-1], 16))
+    return (0, 0)
+
+
+def mem_info():
+    cdef size_t f = 0, t = 0
+    _check_cuda(sf_mem_get_info(&f, &t))
+    return int(f), int(t)
+
+
+def set_tf32_enabled(bint enable):
+    """Accepted and ignored (reference :2474): the fp32 path always runs
+    true fp32 MFMA; gfx950 has no reduced-precision fp32 matrix mode."""
+    return None
+
+
+cdef class CudaStream:
+    """HIP stream at default priority (reference :608-665)."""
+    cdef void* stream
+    cdef int _device_id
+
+    def __cinit__(self, int device_id=0, bint non_blocking=True):
+        self.stream = NULL
+        self._device_id = device_id
+        _check_cuda(sf_stream_create(&self.stream))
+
+    def __dealloc__(self):
+        if self.stream != NULL:
+            sf_stream_destroy(self.stream)
+            self.stream = NULL
+
+    def synchronize(self):
+        _check_cuda(sf_stream_synchronize(self.stream))
+
+    def wait_event(self, CudaEvent event):
+        _check_cuda(sf_stream_wait_event(self.stream, event.event))
+
+    @property
+    def cuda_stream(self):
+        return <uintptr_t>self.stream
+
+    @property
+    def device_id(self):
+        return self._device_id
+
+
+cdef class CudaEvent:
+    """HIP event with timing (reference :646-673)."""
+    cdef void* event
+
+    def __cinit__(self, bint enable_timing=True):
+        self.event = NULL
+        _check_cuda(sf_event_create(&self.event))
+
+    def __dealloc__(self):
+        if self.event != NULL:
+            sf_event_destroy(self.event)
+            self.event = NULL
+
+    def record(self, stream=None):
+        cdef void* s = NULL
+        if stream is not None:
+            s = <void*><uintptr_t>(stream.cuda_stream)
+        _check_cuda(sf_event_record(self.event, s))
+
+    def synchronize(self):
+        _check_cuda(sf_event_synchronize(self.event))
+
+    def elapsed_time(self, CudaEvent end):
+        cdef float ms = 0
+        _check_cuda(sf_event_elapsed_ms(&ms, self.event, end.event))
+        return ms
+
+
+# ================================================================
+#  GEMM family (reference :1088-1190, :1278-1302)
+# ================================================================
+
+cdef object _same_dtype(a, b, str name):
+    if a.dtype != b.dtype:
+        raise TypeError("%s: operand dtypes differ (%s vs %s)" % (name, a.dtype, b.dtype))
+    return a.dtype
+
+
+cdef object _gemm(int transB, int64_t M, int64_t N, int64_t K, int64_t batch,
+                  a, int64_t strideA, b, int64_t ldb, int64_t strideB,
+                  tuple out_shape, float alpha, bias, int epi):
+    dt = a.dtype
+    cdef sf_dtype sdt = _sf_dtype(dt)
+    cdef int dev = a.device_id
+    out = _alloc_like(out_shape, dt, dev)
+    cdef void* pa = _ptr(a)
+    cdef void* pb = _ptr(b)
+    cdef void* pc = _ptr(out)
+    cdef void* pbias = NULL
+    if bias is not None:
+        pbias = _ptr(bias)
+    cdef int ret
+    cdef int64_t lda = K if K > 0 else 1
+    if transB and ldb < 1:
+        ldb = 1
+    with nogil:
+        ret = sf_gemm(0, transB, M, N, K, batch, pa, lda, strideA, pb, ldb, strideB,
+                      pc, N, M * N, sdt, sdt, alpha, pbias, <sf_epilogue>epi, NULL)
+    _check_kernel(ret)
+    return out
+
+
+def gemm_plan(int transB, int64_t M, int64_t N, int64_t K, int64_t batch,
+              uintptr_t ptr_a, int64_t lda, int64_t stride_a,
+              uintptr_t ptr_b, int64_t ldb, int64_t stride_b,
+              int64_t ldc, int64_t stride_c, dtype, out_dtype=None, int epi=0,
+              uintptr_t ptr_bias=0, int transA=0):
+    """Name of the kernel sf_gemm would launch for these arguments (host
+    only; pointers are plain integers and are never dereferenced)."""
+    cdef char buf[128]
+    cdef sf_dtype ab = _sf_dtype(resolve_dtype(dtype))
+    cdef sf_dtype c = _sf_dtype(resolve_dtype(out_dtype)) if out_dtype is not None else ab
+    cdef int ret = sf_gemm_plan(transA, transB, M, N, K, batch, <void*>ptr_a, lda, stride_a,
+                                <void*>ptr_b, ldb, stride_b, NULL, ldc, stride_c, ab, c, 1.0,
+                                <void*>ptr_bias, <sf_epilogue>epi, buf, 128)
+    _check_kernel(ret)
+    return buf.decode('utf-8')
+
+
+def dev_matmul(gt_a, gt_b):
+    """C = A @ B, A (M,K), B (K,N)  (reference :1088-1102)."""
+    _same_dtype(gt_a, gt_b, 'dev_matmul')
+    if len(gt_a.shape) != 2 or len(gt_b.shape) != 2:
+        raise ValueError("dev_matmul expects 2-D operands")
+    cdef int64_t M = gt_a.shape[0], K = gt_a.shape[1], N = gt_b.shape[1]
+    if gt_b.shape[0] != K:
+        raise ValueError("dev_matmul: shapes %s and %s not aligned" % (gt_a.shape, gt_b.shape))
+    return _gemm(0, M, N, K, 1, gt_a, 0, gt_b, N, 0, (M, N), 1.0, None, SF_EPI_NONE)
+
+
+def dev_matmul_nt(gt_a, gt_b, float alpha=1.0):
+    """C = alpha * A @ B^T, A (M,K), B (N,K)  (reference :1105-1119)."""
+    _same_dtype(gt_a, gt_b, 'dev_matmul_nt')
+    if len(gt_a.shape) != 2 or len(gt_b.shape) != 2:
+        raise ValueError("dev_matmul_nt expects 2-D operands")
+    cdef int64_t M = gt_a.shape[0], K = gt_a.shape[1], N = gt_b.shape[0]
+    if gt_b.shape[1] != K:
+        raise ValueError("dev_matmul_nt: shapes %s and %s not aligned" % (gt_a.shape, gt_b.shape))
+    return _gemm(1, M, N, K, 1, gt_a, 0, gt_b, K, 0, (M, N), alpha, None, SF_EPI_NONE)
+
+
+cdef tuple _batch_layout(tuple a_shape, tuple b_shape, int64_t a_mat, int64_t b_mat, str name):
+    """Batch size, operand batch strides and batch shape under np.matmul's
+    rule for the cases this path meets: equal batch dims, or a 2-D operand
+    broadcast over the other's batch."""
+    a_b = a_shape[:-2]
+    b_b = b_shape[:-2]
+    if a_b == b_b:
+        bshape = a_b
+        sa, sb = a_mat, b_mat
+    elif len(b_b) == 0:
+        bshape = a_b
+        sa, sb = a_mat, 0
+    elif len(a_b) == 0:
+        bshape = b_b
+        sa, sb = 0, b_mat
+    else:
+        raise ValueError("%s: batch dims %s and %s do not match" % (name, a_b, b_b))
+    cdef int64_t batch = 1
+    for s in bshape:
+        batch *= s
+    return batch, sa, sb, tuple(bshape)
+
+
+def dev_batched_matmul(gt_a, gt_b):
+    """C[...] = A[...] @ B[...], A (...,M,K), B (...,K,N)  (reference :1122-1149)."""
+    _same_dtype(gt_a, gt_b, 'dev_batched_matmul')
+    a_shape, b_shape = gt_a.shape, gt_b.shape
+    if len(a_shape) < 2 or len(b_shape) < 2:
+        raise ValueError("dev_batched_matmul expects operands of rank >= 2")
+    cdef int64_t M = a_shape[-2], K = a_shape[-1], N = b_shape[-1]
+    if b_shape[-2] != K:
+        raise ValueError("dev_batched_matmul: shapes %s and %s not aligned" % (a_shape, b_shape))
+    batch, sa, sb, bshape = _batch_layout(a_shape, b_shape, M * K, K * N, 'dev_batched_matmul')
+    return _gemm(0, M, N, K, batch, gt_a, sa, gt_b, N, sb, bshape + (M, N), 1.0, None, SF_EPI_NONE)
+
+
+def dev_batched_matmul_nt(gt_a, gt_b, float alpha=1.0):
+    """C[...] = alpha * A[...] @ B[...]^T, A (...,M,K), B (...,N,K), one
+    strided-batched launch (the reference loops over the batch in Python,
+    :1152-1190)."""
+    _same_dtype(gt_a, gt_b, 'dev_batched_matmul_nt')
+    a_shape, b_shape = gt_a.shape, gt_b.shape
+    if len(a_shape) < 2 or len(b_shape) < 2:
+        raise ValueError("dev_batched_matmul_nt expects operands of rank >= 2")
+    cdef int64_t M = a_shape[-2], K = a_shape[-1], N = b_shape[-2]
+    if b_shape[-1] != K:
+        raise ValueError("dev_batched_matmul_nt: shapes %s and %s not aligned" % (a_shape, b_shape))
+    batch, sa, sb, bshape = _batch_layout(a_shape, b_shape, M * K, N * K, 'dev_batched_matmul_nt')
+    return _gemm(1, M, N, K, batch, gt_a, sa, gt_b, K, sb, bshape + (M, N), alpha, None, SF_EPI_NONE)
+
+
+_ACTS = {None: 0, 'none': 0, 'silu': 1, 'gelu': 2, 'gelu_tanh': 2}
+
+
+def dev_linear_forward(gt_x, gt_weight, gt_bias=None, activation=None):
+    """y = act(x @ W^T + b), one fused launch  (reference :1278-1302, which
+    runs SGEMM then a bias pass; SiLU/GELU were further passes).
+    x (..., K), W (N, K), b (N,) -> y (..., N)."""
+    _same_dtype(gt_x, gt_weight, 'dev_linear_forward')
+    if len(gt_x.shape) < 1 or len(gt_weight.shape) != 2:
+        raise ValueError("dev_linear_forward: x must be (..., K) and W (N, K)")
+    cdef int64_t K = gt_x.shape[-1]
+    cdef int64_t N = gt_weight.shape[0]
+    if gt_weight.shape[1] != K:
+        raise ValueError("dev_linear_forward: x %s and W %s not aligned" % (gt_x.shape, gt_weight.shape))
+    cdef int64_t M = gt_x.numel // K if K > 0 else 0
+    if K == 0:
+        M = 1
+        for s in gt_x.shape[:-1]:
+            M *= s
+    if activation not in _ACTS:
+        raise ValueError("dev_linear_forward: unknown activation %r" % (activation,))
+    cdef int act = _ACTS[activation]
+    cdef int epi
+    if gt_bias is not None:
+        if gt_bias.dtype != gt_x.dtype or gt_bias.numel != N:
+            raise ValueError("dev_linear_forward: bias must be (%d,) of the input dtype" % N)
+        epi = (SF_EPI_BIAS, SF_EPI_BIAS_SILU, SF_EPI_BIAS_GELU_TANH)[act]
+    else:
+        epi = (SF_EPI_NONE, SF_EPI_SILU, SF_EPI_GELU_TANH)[act]
+    out_shape = tuple(gt_x.shape[:-1]) + (N,)
+    return _gemm(1, M, N, K, 1, gt_x, 0, gt_weight, K, 0, out_shape, 1.0, gt_bias, epi)
+
+
+def dev_bias_add(gt_c, gt_bias):
+    """In-place C[i, j] += b[j] (reference cuda_bias_add_row_f32)."""
+    cdef int64_t N = gt_c.shape[-1]
+    cdef int64_t M = gt_c.numel // N
+    _check_kernel(sf_bias_add_rows(_ptr(gt_c), _ptr(gt_bias), M, N, _sf_dtype(gt_c.dtype), NULL))
+    return gt_c
+
+
+# ================================================================
+#  Elementwise / softmax (reference :944-948, :990-998, :1016-1034)
+# ================================================================
+
+def dev_silu(gt):
+    out = _alloc_like(gt.shape, gt.dtype, gt.device_id)
+    _check_kernel(sf_silu(_ptr(gt), _ptr(out), gt.numel, _sf_dtype(gt.dtype), NULL))
+    return out
+
+
+def dev_gelu(gt):
+    out = _alloc_like(gt.shape, gt.dtype, gt.device_id)
+    _check_kernel(sf_gelu(_ptr(gt), _ptr(out), gt.numel, _sf_dtype(gt.dtype), NULL))
+    return out
+
+
+def dev_muls(gt, float scalar):
+    out = _alloc_like(gt.shape, gt.dtype, gt.device_id)
+    _check_kernel(sf_muls(_ptr(gt), scalar, _ptr(out), gt.numel, _sf_dtype(gt.dtype), NULL))
+    return out
+
+
+def dev_softmax(gt, int dim=-1, float scale=1.0):
+    """softmax(scale * x) along the last dim."""
+    cdef int ndim = len(gt.shape)
+    if ndim == 0:
+        raise ValueError("dev_softmax: scalar input")
+    if dim != -1 and dim != ndim - 1:
+        raise NotImplementedError("dev_softmax: only the last dim is supported on the device")
+    cdef int64_t cols = gt.shape[ndim - 1]
+    cdef int64_t rows = gt.numel // cols if cols > 0 else 0
+    out = _alloc_like(gt.shape, gt.dtype, gt.device_id)
+    cdef sf_dtype dt = _sf_dtype(gt.dtype)
+    cdef void* px = _ptr(gt)
+    cdef void* py = _ptr(out)
+    cdef int ret
+    with nogil:
+        ret = sf_softmax_rows(px, py, rows, cols, dt, dt, scale, NULL)
+    _check_kernel(ret)
+    return out
+
+
+def dev_scaled_dot_product_attention(q, k, v, scale=None):
+    """softmax(scale * Q K^T) V with the scale folded into the QK^T epilogue:
+    three launches (QK^T, row softmax, PV), scores kept in the input dtype.
+    q, k, v: (..., S, D)  (reference GPU path nn/functional.py:310-321)."""
+    d = q.shape[-1]
+    s = (1.0 / float(d) ** 0.5) if scale is None else float(scale)
+    scores = dev_batched_matmul_nt(q, k, s)
+    probs = dev_softmax(scores, -1)
+    del scores
+    return dev_batched_matmul(probs, v)
+
+
+# ================================================================
+#  Host-array wrappers (reference :2120-2224, :2453-2467): upload, run on
+#  the device, download.
+# ================================================================
+
+def cuda_matmul(cnp.ndarray a not None, cnp.ndarray b not None):
+    ga = gputensor_from_numpy(np.ascontiguousarray(a, dtype=np.float32))
+    gb = gputensor_from_numpy(np.ascontiguousarray(b, dtype=np.float32))
+    return gputensor_to_numpy(dev_matmul(ga, gb))
+
+
+def cuda_matmul_nt(cnp.ndarray a not None, cnp.ndarray b not None):
+    ga = gputensor_from_numpy(np.ascontiguousarray(a, dtype=np.float32))
+    gb = gputensor_from_numpy(np.ascontiguousarray(b, dtype=np.float32))
+    return gputensor_to_numpy(dev_matmul_nt(ga, gb))
+
+
+def cuda_batched_matmul(cnp.ndarray a not None, cnp.ndarray b not None):
+    ga = gputensor_from_numpy(np.ascontiguousarray(a, dtype=np.float32))
+    gb = gputensor_from_numpy(np.ascontiguousarray(b, dtype=np.float32))
+    return gputensor_to_numpy(dev_batched_matmul(ga, gb))
+
+
+def cuda_linear_forward(cnp.ndarray x not None, cnp.ndarray w not None, bias=None):
+    gx = gputensor_from_numpy(np.ascontiguousarray(x, dtype=np.float32))
+    gw = gputensor_from_numpy(np.ascontiguousarray(w, dtype=np.float32))
+    gb = None
+    if bias is not None:
+        gb = gputensor_from_numpy(np.ascontiguousarray(bias, dtype=np.float32))
+    return gputensor_to_numpy(dev_linear_forward(gx, gw, gb))
+
+
+def library_version():
+    return sf_version()

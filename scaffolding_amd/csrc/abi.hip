@@ -1,0 +1,594 @@
+// abi.hip — the extern "C" surface of libsfgemm (include/sfgemm.h):
+// argument validation, kernel selection, runtime wrappers and the native
+// caching allocator.
+//
+// Validation runs before any HIP call, so argument errors are reported the
+// same way with or without a GPU.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "sf_internal.hpp"
+
+namespace sf {
+
+static thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return SF_OK;
+  if (e == hipErrorOutOfMemory) return fail(SF_ERR_OOM, "%s: %s", what, hipGetErrorString(e));
+  if (e == hipErrorNoDevice || e == hipErrorInvalidDevice)
+    return fail(SF_ERR_NO_DEVICE, "%s: %s", what, hipGetErrorString(e));
+  return fail(SF_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int check_launch(const char* what) { return check_hip(hipGetLastError(), what); }
+
+const char* tile_name(int cfg) {
+  switch (cfg) {
+    case TILE_256x256: return "gemm tile 256x256";
+    case TILE_256x128: return "gemm tile 256x128";
+    case TILE_128x128: return "gemm tile 128x128";
+    case TILE_256x64: return "gemm tile 256x64";
+    case TILE_64x64: return "gemm tile 64x64";
+    case TILE_GENERIC: return "gemm tile generic";
+    case TILE_SKINNY: return "gemm skinny";
+  }
+  return "gemm";
+}
+
+void tile_dims(int cfg, bool fp32, int& bm, int& bn) {
+  switch (cfg) {
+    case TILE_256x256: bm = 256; bn = 256; return;
+    case TILE_256x128: bm = 256; bn = 128; return;
+    case TILE_128x128: bm = 128; bn = 128; return;
+    case TILE_256x64: bm = 256; bn = 64; return;
+    case TILE_SKINNY: bm = 16; bn = 32; return;
+    default: bm = 64; bn = 64; return;
+  }
+  (void)fp32;
+}
+
+int launch_gemm16(sf_dtype in, sf_dtype out, bool b_kmajor, int cfg, const GemmParams& p,
+                  int64_t batch, hipStream_t st) {
+  unsigned gx;
+  if (cfg == TILE_SKINNY)
+    gx = static_cast<unsigned>((p.N + 31) / 32);
+  else
+    gx = static_cast<unsigned>(p.tiles_m) * static_cast<unsigned>(p.tiles_n);
+  for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
+    const int64_t nb = (batch - b0) < 65535 ? (batch - b0) : 65535;
+    GemmParams q = p;
+    q.A = static_cast<const uint16_t*>(p.A) + b0 * p.sA;
+    q.B = static_cast<const uint16_t*>(p.B) + b0 * p.sB;
+    q.C = static_cast<uint8_t*>(p.C) + b0 * p.sC * (out == SF_F32 ? 4 : 2);
+    const int rc = (in == SF_BF16)
+                       ? launch_gemm16_bf16(out, b_kmajor, cfg, q, gx, static_cast<unsigned>(nb), st)
+                       : launch_gemm16_f16(out, b_kmajor, cfg, q, gx, static_cast<unsigned>(nb), st);
+    if (rc != SF_OK) return rc;
+  }
+  return SF_OK;
+}
+
+// ---------------------------------------------------------------------
+// Device properties cache (CU count drives tile selection).
+// ---------------------------------------------------------------------
+static std::mutex g_props_mu;
+static std::unordered_map<int, int> g_cu_count;
+
+static int cu_count_current() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  std::lock_guard<std::mutex> lk(g_props_mu);
+  auto it = g_cu_count.find(dev);
+  if (it != g_cu_count.end()) return it->second;
+  int cus = 256;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 256;
+  g_cu_count[dev] = cus;
+  return cus;
+}
+
+static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Picks the 16-bit tile config.  Largest tile that still gives every CU at
+// least one tile; narrow-N problems (P.V, N <= 64) use the 256x64 tile.
+static int choose_tile16(int64_t M, int64_t N, int64_t batch, bool vec, bool b_kmajor,
+                         bool f32_out, int cus) {
+  if (!vec) return TILE_GENERIC;
+  if (b_kmajor && M <= 16) return TILE_SKINNY;
+  if (f32_out) return TILE_128x128;
+  auto tiles = [&](int64_t bm, int64_t bn) { return cdiv(M, bm) * cdiv(N, bn) * batch; };
+  if (N <= 64) return tiles(256, 64) >= cus ? TILE_256x64 : TILE_64x64;
+  if (tiles(256, 256) >= cus) return TILE_256x256;
+  if (tiles(256, 128) >= cus) return TILE_256x128;
+  if (tiles(128, 128) >= cus) return TILE_128x128;
+  return TILE_64x64;
+}
+
+static int choose_tile32(int64_t M, int64_t N, int64_t batch, bool vec, int cus) {
+  if (!vec) return TILE_GENERIC;
+  if (cdiv(M, 128) * cdiv(N, 128) * batch >= cus) return TILE_128x128;
+  return TILE_64x64;
+}
+
+static bool valid_dtype(int d) { return d == SF_F32 || d == SF_F16 || d == SF_BF16; }
+static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace sf
+
+using namespace sf;
+
+extern "C" {
+
+const char* sf_status_string(int status) {
+  switch (status) {
+    case SF_OK: return "success";
+    case SF_ERR_HIP: return "HIP runtime error";
+    case SF_ERR_INVALID_ARG: return "invalid argument";
+    case SF_ERR_UNSUPPORTED: return "unsupported operation";
+    case SF_ERR_NO_DEVICE: return "no usable GPU device";
+    case SF_ERR_OOM: return "out of device memory";
+  }
+  return "unknown status";
+}
+
+const char* sf_last_error(void) { return g_err; }
+
+int sf_version(void) { return 100; /* 0.1.0 */ }
+
+// Validates sf_gemm's arguments and fills the launch plan.  Returns SF_OK
+// with *noop = true for an empty problem.  No HIP call before validation.
+struct GemmPlan {
+  GemmParams p;
+  int cfg;
+  bool fp32;
+  bool b_kmajor;
+  bool noop;
+};
+
+static int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t batch,
+                        const void* A, int64_t lda, int64_t strideA, const void* B, int64_t ldb,
+                        int64_t strideB, void* C, int64_t ldc, int64_t strideC, sf_dtype ab_dtype,
+                        sf_dtype c_dtype, float alpha, const void* bias, sf_epilogue epi,
+                        bool need_c, GemmPlan& plan) {
+  g_err[0] = 0;
+  plan.noop = false;
+  if (!valid_dtype(ab_dtype) || !valid_dtype(c_dtype))
+    return fail(SF_ERR_INVALID_ARG, "sf_gemm: unknown dtype (%d, %d)", (int)ab_dtype, (int)c_dtype);
+  if ((int)epi < SF_EPI_NONE || (int)epi > SF_EPI_GELU_TANH)
+    return fail(SF_ERR_INVALID_ARG, "sf_gemm: unknown epilogue %d", (int)epi);
+  if (transA) return fail(SF_ERR_UNSUPPORTED, "sf_gemm: transA is not supported");
+  if (c_dtype != ab_dtype && c_dtype != SF_F32)
+    return fail(SF_ERR_UNSUPPORTED, "sf_gemm: output dtype must equal the input dtype or be F32");
+  if (M < 0 || N < 0 || K < 0 || batch < 0)
+    return fail(SF_ERR_INVALID_ARG, "sf_gemm: negative size (M=%lld N=%lld K=%lld batch=%lld)",
+                (long long)M, (long long)N, (long long)K, (long long)batch);
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
+    return fail(SF_ERR_INVALID_ARG, "sf_gemm: M, N, K must be < 2^31");
+  const bool has_bias = epi_has_bias(epi);
+  if (has_bias && bias == nullptr)
+    return fail(SF_ERR_INVALID_ARG, "sf_gemm: epilogue %d needs a bias pointer", (int)epi);
+  if (!has_bias && bias != nullptr)
+    return fail(SF_ERR_INVALID_ARG, "sf_gemm: bias given but epilogue %d has no bias", (int)epi);
+  if (M == 0 || N == 0 || batch == 0) {
+    plan.noop = true;
+    return SF_OK;
+  }
+  const bool b_kmajor = transB != 0;
+  if ((need_c && C == nullptr) || (K > 0 && (A == nullptr || B == nullptr)))
+    return fail(SF_ERR_INVALID_ARG, "sf_gemm: null operand pointer");
+  if (lda < (K > 0 ? K : 1) || ldb < (b_kmajor ? (K > 0 ? K : 1) : N) || ldc < N)
+    return fail(SF_ERR_INVALID_ARG,
+                "sf_gemm: leading dimension too small (lda=%lld ldb=%lld ldc=%lld for M=%lld "
+                "N=%lld K=%lld transB=%d)",
+                (long long)lda, (long long)ldb, (long long)ldc, (long long)M, (long long)N,
+                (long long)K, transB);
+  if (strideA < 0 || strideB < 0 || strideC < 0)
+    return fail(SF_ERR_INVALID_ARG, "sf_gemm: negative batch stride");
+  if (batch > 1 && strideC < (M - 1) * ldc + N)
+    return fail(SF_ERR_INVALID_ARG, "sf_gemm: strideC=%lld overlaps batch entries (need >= %lld)",
+                (long long)strideC, (long long)((M - 1) * ldc + N));
+
+  GemmParams& p = plan.p;
+  p.A = A; p.B = B; p.C = C; p.bias = bias;
+  p.lda = lda; p.ldb = ldb; p.ldc = ldc;
+  p.sA = strideA; p.sB = strideB; p.sC = strideC;
+  p.M = (int)M; p.N = (int)N; p.K = (int)K;
+  p.alpha = alpha;
+  p.epi = (int)epi;
+  plan.b_kmajor = b_kmajor;
+  const int cus = cu_count_current();
+  int bm, bn;
+  if (ab_dtype == SF_F32) {
+    const bool vec = al16(A) && al16(B) && (lda % 4 == 0) && (ldb % 4 == 0) &&
+                     (strideA % 4 == 0) && (strideB % 4 == 0) && (K % 4 == 0) &&
+                     (b_kmajor || N % 4 == 0);
+    plan.fp32 = true;
+    plan.cfg = choose_tile32(M, N, batch, vec, cus);
+  } else {
+    const bool vec = al16(A) && al16(B) && (lda % 8 == 0) && (ldb % 8 == 0) &&
+                     (strideA % 8 == 0) && (strideB % 8 == 0) && (K % 8 == 0) &&
+                     (b_kmajor || N % 8 == 0);
+    plan.fp32 = false;
+    plan.cfg = choose_tile16(M, N, batch, vec, b_kmajor, c_dtype == SF_F32, cus);
+  }
+  tile_dims(plan.cfg, plan.fp32, bm, bn);
+  if (cdiv(M, bm) * cdiv(N, bn) > INT32_MAX)
+    return fail(SF_ERR_UNSUPPORTED, "sf_gemm: %lld x %lld output needs more than 2^31 tiles",
+                (long long)M, (long long)N);
+  p.tiles_m = (int)cdiv(M, bm);
+  p.tiles_n = (int)cdiv(N, bn);
+  return SF_OK;
+}
+
+int sf_gemm(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t batch, const void* A,
+            int64_t lda, int64_t strideA, const void* B, int64_t ldb, int64_t strideB, void* C,
+            int64_t ldc, int64_t strideC, sf_dtype ab_dtype, sf_dtype c_dtype, float alpha,
+            const void* bias, sf_epilogue epi, void* stream) {
+  GemmPlan plan;
+  int rc = gemm_prepare(transA, transB, M, N, K, batch, A, lda, strideA, B, ldb, strideB, C, ldc,
+                        strideC, ab_dtype, c_dtype, alpha, bias, epi, true, plan);
+  if (rc != SF_OK || plan.noop) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (plan.fp32) return launch_gemm32(plan.b_kmajor, plan.cfg, plan.p, batch, st);
+  return launch_gemm16(ab_dtype, c_dtype, plan.b_kmajor, plan.cfg, plan.p, batch, st);
+}
+
+int sf_gemm_plan(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t batch,
+                 const void* A, int64_t lda, int64_t strideA, const void* B, int64_t ldb,
+                 int64_t strideB, void* C, int64_t ldc, int64_t strideC, sf_dtype ab_dtype,
+                 sf_dtype c_dtype, float alpha, const void* bias, sf_epilogue epi, char* buf,
+                 int len) {
+  if (buf == nullptr || len <= 0) return fail(SF_ERR_INVALID_ARG, "sf_gemm_plan: bad buffer");
+  buf[0] = 0;
+  GemmPlan plan;
+  int rc = gemm_prepare(transA, transB, M, N, K, batch, A, lda, strideA, B, ldb, strideB, C, ldc,
+                        strideC, ab_dtype, c_dtype, alpha, bias, epi, false, plan);
+  if (rc != SF_OK) return rc;
+  snprintf(buf, (size_t)len, "%s%s", plan.noop ? "noop" : tile_name(plan.cfg),
+           plan.noop ? "" : (plan.fp32 ? " fp32" : " 16-bit"));
+  return SF_OK;
+}
+
+int sf_softmax_rows(const void* x, void* y, int64_t rows, int64_t cols, sf_dtype in_dtype,
+                    sf_dtype out_dtype, float scale, void* stream) {
+  g_err[0] = 0;
+  if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype))
+    return fail(SF_ERR_INVALID_ARG, "sf_softmax_rows: unknown dtype");
+  if (rows < 0 || cols < 0) return fail(SF_ERR_INVALID_ARG, "sf_softmax_rows: negative size");
+  if (rows > INT32_MAX || cols > INT32_MAX)
+    return fail(SF_ERR_INVALID_ARG, "sf_softmax_rows: rows and cols must be < 2^31");
+  if (rows == 0 || cols == 0) return SF_OK;
+  if (x == nullptr || y == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_softmax_rows: null pointer");
+  return launch_softmax(x, y, rows, cols, in_dtype, out_dtype, scale, static_cast<hipStream_t>(stream));
+}
+
+static int unary_common(int op, const void* x, void* y, int64_t n, sf_dtype dt, float s,
+                        void* stream, const char* name) {
+  g_err[0] = 0;
+  if (!valid_dtype(dt)) return fail(SF_ERR_INVALID_ARG, "%s: unknown dtype", name);
+  if (n < 0) return fail(SF_ERR_INVALID_ARG, "%s: negative size", name);
+  if (n == 0) return SF_OK;
+  if (x == nullptr || y == nullptr) return fail(SF_ERR_INVALID_ARG, "%s: null pointer", name);
+  return launch_unary(op, x, y, n, dt, s, static_cast<hipStream_t>(stream));
+}
+
+int sf_silu(const void* x, void* y, int64_t n, sf_dtype dt, void* stream) {
+  return unary_common(0, x, y, n, dt, 1.0f, stream, "sf_silu");
+}
+int sf_gelu(const void* x, void* y, int64_t n, sf_dtype dt, void* stream) {
+  return unary_common(1, x, y, n, dt, 1.0f, stream, "sf_gelu");
+}
+int sf_muls(const void* x, float s, void* y, int64_t n, sf_dtype dt, void* stream) {
+  return unary_common(2, x, y, n, dt, s, stream, "sf_muls");
+}
+
+int sf_bias_add_rows(void* C, const void* bias, int64_t M, int64_t N, sf_dtype dt, void* stream) {
+  g_err[0] = 0;
+  if (!valid_dtype(dt)) return fail(SF_ERR_INVALID_ARG, "sf_bias_add_rows: unknown dtype");
+  if (M < 0 || N < 0) return fail(SF_ERR_INVALID_ARG, "sf_bias_add_rows: negative size");
+  if (M == 0 || N == 0) return SF_OK;
+  if (C == nullptr || bias == nullptr)
+    return fail(SF_ERR_INVALID_ARG, "sf_bias_add_rows: null pointer");
+  return launch_bias_rows(C, bias, M, N, dt, static_cast<hipStream_t>(stream));
+}
+
+int sf_cast(const void* x, sf_dtype in_dtype, void* y, sf_dtype out_dtype, int64_t n, void* stream) {
+  g_err[0] = 0;
+  if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype))
+    return fail(SF_ERR_INVALID_ARG, "sf_cast: unknown dtype");
+  if (n < 0) return fail(SF_ERR_INVALID_ARG, "sf_cast: negative size");
+  if (n == 0) return SF_OK;
+  if (x == nullptr || y == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_cast: null pointer");
+  return launch_cast(x, in_dtype, y, out_dtype, n, static_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------------
+// Runtime
+// ---------------------------------------------------------------------
+int sf_get_device_count(int* count) {
+  if (count == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_get_device_count: null pointer");
+  *count = 0;
+  hipError_t e = hipGetDeviceCount(count);
+  if (e == hipErrorNoDevice) {
+    *count = 0;
+    return SF_OK;
+  }
+  if (e != hipSuccess) *count = 0;
+  return check_hip(e, "hipGetDeviceCount");
+}
+
+int sf_set_device(int device) { return check_hip(hipSetDevice(device), "hipSetDevice"); }
+
+int sf_get_device(int* device) {
+  if (device == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_get_device: null pointer");
+  return check_hip(hipGetDevice(device), "hipGetDevice");
+}
+
+int sf_device_synchronize(void) { return check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize"); }
+
+int sf_get_device_name(int device, char* buf, int len) {
+  if (buf == nullptr || len <= 0) return fail(SF_ERR_INVALID_ARG, "sf_get_device_name: bad buffer");
+  hipDeviceProp_t prop;
+  int rc = check_hip(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+  if (rc != SF_OK) return rc;
+  snprintf(buf, (size_t)len, "%s", prop.name);
+  return SF_OK;
+}
+
+int sf_get_device_arch(int device, char* buf, int len) {
+  if (buf == nullptr || len <= 0) return fail(SF_ERR_INVALID_ARG, "sf_get_device_arch: bad buffer");
+  hipDeviceProp_t prop;
+  int rc = check_hip(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+  if (rc != SF_OK) return rc;
+  snprintf(buf, (size_t)len, "%s", prop.gcnArchName);
+  return SF_OK;
+}
+
+int sf_get_device_props(int device, int* cu_count, int64_t* total_mem, int* clock_khz,
+                        int* l2_bytes) {
+  hipDeviceProp_t prop;
+  int rc = check_hip(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+  if (rc != SF_OK) return rc;
+  if (cu_count) *cu_count = prop.multiProcessorCount;
+  if (total_mem) *total_mem = (int64_t)prop.totalGlobalMem;
+  if (clock_khz) *clock_khz = prop.clockRate;
+  if (l2_bytes) *l2_bytes = prop.l2CacheSize;
+  return SF_OK;
+}
+
+int sf_mem_get_info(size_t* free_bytes, size_t* total_bytes) {
+  if (free_bytes == nullptr || total_bytes == nullptr)
+    return fail(SF_ERR_INVALID_ARG, "sf_mem_get_info: null pointer");
+  return check_hip(hipMemGetInfo(free_bytes, total_bytes), "hipMemGetInfo");
+}
+
+int sf_malloc(void** ptr, size_t nbytes) {
+  if (ptr == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_malloc: null pointer");
+  *ptr = nullptr;
+  return check_hip(hipMalloc(ptr, nbytes ? nbytes : 1), "hipMalloc");
+}
+
+int sf_free(void* ptr) { return check_hip(hipFree(ptr), "hipFree"); }
+
+// ---------------------------------------------------------------------
+// Caching allocator: per-device free lists keyed by the 256-byte-rounded
+// size.  A freed block is kept for reuse unless the device's pooled bytes
+// would exceed the limit (default 16 GiB of the 288 GB HBM), in which case
+// it is returned with hipFree.  An allocation that fails with
+// out-of-memory empties that device's pool and retries once.
+// ---------------------------------------------------------------------
+namespace {
+struct Pool {
+  std::unordered_map<size_t, std::vector<void*>> free_lists;
+  size_t pooled = 0;
+  size_t live = 0;
+};
+std::mutex g_pool_mu;
+std::unordered_map<int, Pool> g_pools;
+size_t g_pool_limit = size_t(16) << 30;
+
+size_t round256(size_t n) { return n == 0 ? 256 : (n + 255) & ~size_t(255); }
+
+// Frees every pooled block of `dev` (caller holds the lock and has made
+// `dev` current).
+void drain_pool(Pool& pool) {
+  for (auto& kv : pool.free_lists)
+    for (void* p : kv.second) (void)hipFree(p);
+  pool.free_lists.clear();
+  pool.pooled = 0;
+}
+
+struct DeviceGuard {
+  int prev = -1;
+  bool switched = false;
+  int enter(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) {
+      int rc = check_hip(hipSetDevice(dev), "hipSetDevice");
+      if (rc != SF_OK) return rc;
+      switched = true;
+    }
+    return SF_OK;
+  }
+  ~DeviceGuard() {
+    if (switched && prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+}  // namespace
+
+int sf_cache_alloc(int device, size_t nbytes, void** ptr, size_t* got_bytes) {
+  if (ptr == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_cache_alloc: null pointer");
+  *ptr = nullptr;
+  const size_t sz = round256(nbytes);
+  std::lock_guard<std::mutex> lk(g_pool_mu);
+  Pool& pool = g_pools[device];
+  auto it = pool.free_lists.find(sz);
+  if (it != pool.free_lists.end() && !it->second.empty()) {
+    *ptr = it->second.back();
+    it->second.pop_back();
+    pool.pooled -= sz;
+    pool.live += sz;
+    if (got_bytes) *got_bytes = sz;
+    return SF_OK;
+  }
+  DeviceGuard g;
+  int rc = g.enter(device);
+  if (rc != SF_OK) return rc;
+  hipError_t e = hipMalloc(ptr, sz);
+  if (e == hipErrorOutOfMemory && pool.pooled > 0) {
+    (void)hipGetLastError();
+    drain_pool(pool);
+    e = hipMalloc(ptr, sz);
+  }
+  if (e != hipSuccess) {
+    *ptr = nullptr;
+    return check_hip(e, "hipMalloc (caching allocator)");
+  }
+  pool.live += sz;
+  if (got_bytes) *got_bytes = sz;
+  return SF_OK;
+}
+
+int sf_cache_free(int device, void* ptr, size_t nbytes) {
+  if (ptr == nullptr) return SF_OK;
+  const size_t sz = round256(nbytes);
+  std::lock_guard<std::mutex> lk(g_pool_mu);
+  Pool& pool = g_pools[device];
+  pool.live = pool.live >= sz ? pool.live - sz : 0;
+  if (pool.pooled + sz > g_pool_limit) {
+    DeviceGuard g;
+    int rc = g.enter(device);
+    if (rc != SF_OK) return rc;
+    return check_hip(hipFree(ptr), "hipFree (caching allocator)");
+  }
+  pool.free_lists[sz].push_back(ptr);
+  pool.pooled += sz;
+  return SF_OK;
+}
+
+int sf_cache_empty(int device) {
+  std::lock_guard<std::mutex> lk(g_pool_mu);
+  for (auto& kv : g_pools) {
+    if (device >= 0 && kv.first != device) continue;
+    DeviceGuard g;
+    int rc = g.enter(kv.first);
+    if (rc != SF_OK) return rc;
+    drain_pool(kv.second);
+  }
+  return SF_OK;
+}
+
+int sf_cache_stats(int device, size_t* pooled_bytes, size_t* live_bytes) {
+  std::lock_guard<std::mutex> lk(g_pool_mu);
+  size_t pooled = 0, live = 0;
+  for (auto& kv : g_pools) {
+    if (device >= 0 && kv.first != device) continue;
+    pooled += kv.second.pooled;
+    live += kv.second.live;
+  }
+  if (pooled_bytes) *pooled_bytes = pooled;
+  if (live_bytes) *live_bytes = live;
+  return SF_OK;
+}
+
+int sf_cache_set_limit(size_t bytes_per_device) {
+  std::lock_guard<std::mutex> lk(g_pool_mu);
+  g_pool_limit = bytes_per_device;
+  return SF_OK;
+}
+
+int sf_memcpy_h2d(void* dst, const void* src, size_t nbytes, void* stream) {
+  if (nbytes == 0) return SF_OK;
+  if (dst == nullptr || src == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_memcpy_h2d: null pointer");
+  if (stream == nullptr) return check_hip(hipMemcpy(dst, src, nbytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+  return check_hip(hipMemcpyAsync(dst, src, nbytes, hipMemcpyHostToDevice, (hipStream_t)stream),
+                   "hipMemcpyAsync H2D");
+}
+
+int sf_memcpy_d2h(void* dst, const void* src, size_t nbytes, void* stream) {
+  if (nbytes == 0) return SF_OK;
+  if (dst == nullptr || src == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_memcpy_d2h: null pointer");
+  if (stream == nullptr) return check_hip(hipMemcpy(dst, src, nbytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+  return check_hip(hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToHost, (hipStream_t)stream),
+                   "hipMemcpyAsync D2H");
+}
+
+int sf_memcpy_d2d(void* dst, const void* src, size_t nbytes, void* stream) {
+  if (nbytes == 0) return SF_OK;
+  if (dst == nullptr || src == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_memcpy_d2d: null pointer");
+  return check_hip(hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToDevice, (hipStream_t)stream),
+                   "hipMemcpyAsync D2D");
+}
+
+int sf_zero(void* dst, size_t nbytes, void* stream) {
+  if (nbytes == 0) return SF_OK;
+  if (dst == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_zero: null pointer");
+  return launch_zero(dst, nbytes, (hipStream_t)stream);
+}
+
+int sf_stream_create(void** stream) {
+  if (stream == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_stream_create: null pointer");
+  hipStream_t s = nullptr;
+  int rc = check_hip(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+  *stream = s;
+  return rc;
+}
+
+int sf_stream_destroy(void* stream) {
+  if (stream == nullptr) return SF_OK;
+  return check_hip(hipStreamDestroy((hipStream_t)stream), "hipStreamDestroy");
+}
+
+int sf_stream_synchronize(void* stream) {
+  return check_hip(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+}
+
+int sf_event_create(void** event) {
+  if (event == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_event_create: null pointer");
+  hipEvent_t e = nullptr;
+  int rc = check_hip(hipEventCreate(&e), "hipEventCreate");
+  *event = e;
+  return rc;
+}
+
+int sf_event_destroy(void* event) {
+  if (event == nullptr) return SF_OK;
+  return check_hip(hipEventDestroy((hipEvent_t)event), "hipEventDestroy");
+}
+
+int sf_event_record(void* event, void* stream) {
+  if (event == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_event_record: null event");
+  return check_hip(hipEventRecord((hipEvent_t)event, (hipStream_t)stream), "hipEventRecord");
+}
+
+int sf_event_synchronize(void* event) {
+  if (event == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_event_synchronize: null event");
+  return check_hip(hipEventSynchronize((hipEvent_t)event), "hipEventSynchronize");
+}
+
+int sf_stream_wait_event(void* stream, void* event) {
+  if (event == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_stream_wait_event: null event");
+  return check_hip(hipStreamWaitEvent((hipStream_t)stream, (hipEvent_t)event, 0), "hipStreamWaitEvent");
+}
+
+int sf_event_elapsed_ms(float* ms, void* start, void* end) {
+  if (ms == nullptr || start == nullptr || end == nullptr)
+    return fail(SF_ERR_INVALID_ARG, "sf_event_elapsed_ms: null pointer");
+  return check_hip(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end), "hipEventElapsedTime");
+}
+
+}  // extern "C"

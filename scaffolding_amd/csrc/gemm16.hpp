@@ -1,0 +1,321 @@
+// gemm16.hpp — 16-bit (bf16 / fp16) GEMM on gfx950 MFMA with fp32
+// accumulation and a register-fused epilogue.
+//
+//   C[b] = epi(alpha * A[b] . op(B[b]) (+ bias))      row-major
+//
+// A is M x K (K-contiguous).  B is either N x K (K-contiguous, "NT":
+// x . W^T, QK^T) or K x N (N-contiguous, "NN": A . B, P . V).
+//
+// Work decomposition
+//   * one workgroup per BM x BN output tile, grid.y = batch;
+//   * WAVES_M x WAVES_N waves, each owning a WM x WN sub-tile computed as
+//     (WN/16) x (WM/16) blocks of v_mfma_f32_16x16x32_{bf16,f16};
+//   * K walked in BK = 64 slices, double-buffered in LDS: while the MFMAs
+//     consume slice k from one buffer, the 16-byte global loads of slice k+1
+//     are in flight into registers and land in the other buffer after the
+//     MFMAs, so one barrier per slice suffices.
+//
+// MFMA operand roles.  The MFMA computes D = X . Y with X lane l holding
+// row (l%16) and Y lane l holding column (l%16); lane l receives
+// D[4*(l/16)+q][l%16], q = 0..3.  This kernel feeds X from the B tile
+// (rows = output columns n) and Y from the A tile (columns = output rows m),
+// so lane l ends with C[m = l%16][n = 4*(l/16) + 0..3]: four consecutive
+// output columns, i.e. one 8-byte (16-bit out) or 16-byte (fp32 out) store
+// and one vector bias load per fragment.
+//
+// LDS layout.  Both tiles are stored K-contiguous, 64 elements (128 bytes)
+// per row, as eight 16-byte chunks; chunk c of row r sits at slot
+// c ^ (r & 7).  An MFMA operand read (16 lanes on 16 consecutive rows, same
+// chunk) therefore touches 8 distinct slots per 8 lanes — no bank conflicts
+// for ds_read_b128 — and the 16-byte global->LDS stores of a row are a
+// permutation of the row's slots.  An N-contiguous B tile is transposed on
+// its way into LDS (each 16-byte global load of 8 consecutive n scatters
+// into 8 rows); the lane->k assignment makes each ds_write_b16 instruction
+// cover 64 distinct 2-byte slots of one 128-byte row group.
+#pragma once
+
+#include "sf_common.hpp"
+
+namespace sf {
+
+struct GemmParams {
+  const void* A;
+  const void* B;
+  void* C;
+  const void* bias;
+  int64_t lda, ldb, ldc;
+  int64_t sA, sB, sC;  // batch strides, elements (0 = broadcast)
+  int M, N, K;
+  float alpha;
+  int epi;  // sf_epilogue
+  int tiles_m, tiles_n;
+};
+
+template <typename T> struct Mfma16;
+template <> struct Mfma16<BF16> {
+  __device__ __forceinline__ static f32x4 run(u32x4 x, u32x4 y, f32x4 acc) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x),
+                                                   __builtin_bit_cast(bf16x8, y), acc, 0, 0, 0);
+  }
+};
+template <> struct Mfma16<F16> {
+  __device__ __forceinline__ static f32x4 run(u32x4 x, u32x4 y, f32x4 acc) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, x),
+                                                  __builtin_bit_cast(f16x8, y), acc, 0, 0, 0);
+  }
+};
+
+// Byte offset of (row, 16-byte chunk) inside a swizzled 128-byte-row tile.
+__device__ __forceinline__ int swz(int row, int chunk) {
+  return (row << 7) + (((chunk ^ (row & 7))) << 4);
+}
+
+// Store four fp32 results (already through the epilogue) to C[m][n..n+3].
+template <typename TOut> struct Store4 {  // 16-bit outputs
+  __device__ __forceinline__ static void run(uint16_t* crow, int n, int N, bool vec_ok,
+                                             const float v[4]) {
+    uint16_t h[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) h[q] = Elem<TOut>::from_f32(v[q]);
+    if (vec_ok && n + 3 < N) {
+      u32x2 o = {static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16),
+                 static_cast<uint32_t>(h[2]) | (static_cast<uint32_t>(h[3]) << 16)};
+      *reinterpret_cast<u32x2*>(crow + n) = o;
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (n + q < N) crow[n + q] = h[q];
+    }
+  }
+};
+template <> struct Store4<float> {
+  __device__ __forceinline__ static void run(float* crow, int n, int N, bool vec_ok,
+                                             const float v[4]) {
+    if (vec_ok && n + 3 < N) {
+      f32x4 o = {v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<f32x4*>(crow + n) = o;
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (n + q < N) crow[n + q] = v[q];
+    }
+  }
+};
+
+// Bias values for columns n..n+3 (bias dtype = input dtype TIn), fp32.
+template <typename TIn>
+__device__ __forceinline__ void load_bias4(const void* bias, int n, int N, float b[4]) {
+  const uint16_t* bp = static_cast<const uint16_t*>(bias);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) b[q] = (n + q < N) ? Elem<TIn>::to_f32(bp[n + q]) : 0.0f;
+}
+
+template <typename TIn, typename TOut, int BM, int BN, int WAVES_M, int WAVES_N, bool B_KMAJOR,
+          bool VEC>
+__global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmParams p) {
+  constexpr int NT = WAVES_M * WAVES_N * 64;
+  constexpr int BK = 64;
+  constexpr int CH = BK / 8;  // 16-byte chunks per tile row
+  constexpr int WM = BM / WAVES_M;
+  constexpr int WN = BN / WAVES_N;
+  constexpr int FM = WM / 16;
+  constexpr int FN = WN / 16;
+  constexpr int A_BYTES = BM * BK * 2;
+  constexpr int B_BYTES = BN * BK * 2;
+  constexpr int STAGE = A_BYTES + B_BYTES;
+  static_assert(WM % 16 == 0 && WN % 16 == 0, "wave tile must be 16-aligned");
+  static_assert((BM * CH) % NT == 0, "A tile loads must divide evenly");
+  static_assert((BN * CH) % NT == 0, "B tile loads must divide evenly");
+  constexpr int A_LD = BM * CH / NT;
+  constexpr int B_LD = BN * CH / NT;
+
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WAVES_N;
+  const int wn = wave % WAVES_N;
+
+  int tm, tn;
+  {
+    int pid = xcd_remap(blockIdx.x, gridDim.x);
+    group_tile(pid, p.tiles_m, p.tiles_n, 8, tm, tn);
+  }
+  const int m0 = tm * BM;
+  const int n0 = tn * BN;
+  const int64_t b = blockIdx.y;
+  const uint16_t* __restrict__ A = static_cast<const uint16_t*>(p.A) + b * p.sA;
+  const uint16_t* __restrict__ B = static_cast<const uint16_t*>(p.B) + b * p.sB;
+  const int M = p.M, N = p.N, K = p.K;
+  const int64_t lda = p.lda, ldb = p.ldb;
+
+  f32x4 acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  u32x4 ra[A_LD];
+  u32x4 rb[B_LD];
+
+  // ---- global -> registers ------------------------------------------------
+  auto load_tiles = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      int idx = tid + i * NT;
+      int row = idx / CH, ch = idx % CH;
+      int gm = m0 + row, gk = k0 + ch * 8;
+      if constexpr (VEC) {
+        ra[i] = (gm < M && gk < K)
+                    ? *reinterpret_cast<const u32x4*>(A + (int64_t)gm * lda + gk)
+                    : u32x4{0u, 0u, 0u, 0u};
+      } else {
+        uint16_t e[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          e[q] = (gm < M && gk + q < K) ? A[(int64_t)gm * lda + gk + q] : (uint16_t)0;
+        ra[i] = u32x4{e[0] | ((uint32_t)e[1] << 16), e[2] | ((uint32_t)e[3] << 16),
+                      e[4] | ((uint32_t)e[5] << 16), e[6] | ((uint32_t)e[7] << 16)};
+      }
+    }
+    if constexpr (B_KMAJOR) {
+#pragma unroll
+      for (int i = 0; i < B_LD; ++i) {
+        int idx = tid + i * NT;
+        int row = idx / CH, ch = idx % CH;
+        int gn = n0 + row, gk = k0 + ch * 8;
+        if constexpr (VEC) {
+          rb[i] = (gn < N && gk < K)
+                      ? *reinterpret_cast<const u32x4*>(B + (int64_t)gn * ldb + gk)
+                      : u32x4{0u, 0u, 0u, 0u};
+        } else {
+          uint16_t e[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q)
+            e[q] = (gn < N && gk + q < K) ? B[(int64_t)gn * ldb + gk + q] : (uint16_t)0;
+          rb[i] = u32x4{e[0] | ((uint32_t)e[1] << 16), e[2] | ((uint32_t)e[3] << 16),
+                        e[4] | ((uint32_t)e[5] << 16), e[6] | ((uint32_t)e[7] << 16)};
+        }
+      }
+    } else {
+      // B is K x N: thread -> (k = idx % BK, 8-wide n chunk = idx / BK).
+#pragma unroll
+      for (int i = 0; i < B_LD; ++i) {
+        int idx = tid + i * NT;
+        int k = idx % BK, nc = idx / BK;
+        int gk = k0 + k, gn = n0 + nc * 8;
+        if constexpr (VEC) {
+          rb[i] = (gk < K && gn < N)
+                      ? *reinterpret_cast<const u32x4*>(B + (int64_t)gk * ldb + gn)
+                      : u32x4{0u, 0u, 0u, 0u};
+        } else {
+          uint16_t e[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q)
+            e[q] = (gk < K && gn + q < N) ? B[(int64_t)gk * ldb + gn + q] : (uint16_t)0;
+          rb[i] = u32x4{e[0] | ((uint32_t)e[1] << 16), e[2] | ((uint32_t)e[3] << 16),
+                        e[4] | ((uint32_t)e[5] << 16), e[6] | ((uint32_t)e[7] << 16)};
+        }
+      }
+    }
+  };
+
+  // ---- registers -> LDS stage ----------------------------------------------
+  auto store_tiles = [&](int stage) {
+    uint8_t* As = smem + stage * STAGE;
+    uint8_t* Bs = As + A_BYTES;
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      int idx = tid + i * NT;
+      int row = idx / CH, ch = idx % CH;
+      *reinterpret_cast<u32x4*>(As + swz(row, ch)) = ra[i];
+    }
+    if constexpr (B_KMAJOR) {
+#pragma unroll
+      for (int i = 0; i < B_LD; ++i) {
+        int idx = tid + i * NT;
+        int row = idx / CH, ch = idx % CH;
+        *reinterpret_cast<u32x4*>(Bs + swz(row, ch)) = rb[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < B_LD; ++i) {
+        int idx = tid + i * NT;
+        int k = idx % BK, nc = idx / BK;
+        uint32_t w[4] = {rb[i][0], rb[i][1], rb[i][2], rb[i][3]};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          int n = nc * 8 + e;
+          uint16_t v = static_cast<uint16_t>(w[e >> 1] >> ((e & 1) * 16));
+          *reinterpret_cast<uint16_t*>(Bs + swz(n, k >> 3) + ((k & 7) << 1)) = v;
+        }
+      }
+    }
+  };
+
+  // ---- LDS -> MFMA ---------------------------------------------------------
+  auto compute = [&](int stage) {
+    const uint8_t* As = smem + stage * STAGE;
+    const uint8_t* Bs = As + A_BYTES;
+#pragma unroll
+    for (int s = 0; s < BK / 32; ++s) {
+      const int ch = s * 4 + (lane >> 4);
+      u32x4 ya[FM], xb[FN];
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        int row = wm * WM + j * 16 + (lane & 15);
+        ya[j] = *reinterpret_cast<const u32x4*>(As + swz(row, ch));
+      }
+#pragma unroll
+      for (int i = 0; i < FN; ++i) {
+        int row = wn * WN + i * 16 + (lane & 15);
+        xb[i] = *reinterpret_cast<const u32x4*>(Bs + swz(row, ch));
+      }
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j) acc[i][j] = Mfma16<TIn>::run(xb[i], ya[j], acc[i][j]);
+    }
+  };
+
+  const int KT = (K + BK - 1) / BK;
+  if (KT > 0) {
+    load_tiles(0);
+    store_tiles(0);
+    __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) {
+      const bool more = kt + 1 < KT;
+      if (more) load_tiles((kt + 1) * BK);
+      compute(kt & 1);
+      if (more) store_tiles((kt + 1) & 1);
+      __syncthreads();
+    }
+  }
+
+  // ---- epilogue ------------------------------------------------------------
+  typedef typename Elem<TOut>::storage OutS;
+  OutS* C = static_cast<OutS*>(p.C) + b * p.sC;
+  const bool has_bias = epi_has_bias(p.epi);
+  const int act = epi_act(p.epi);
+  const float alpha = p.alpha;
+  const bool vec_ok = ((p.ldc & 3) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
+#pragma unroll
+  for (int i = 0; i < FN; ++i) {
+    const int n = n0 + wn * WN + i * 16 + 4 * (lane >> 4);
+    float bv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (has_bias) load_bias4<TIn>(p.bias, n, N, bv);
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      const int m = m0 + wm * WM + j * 16 + (lane & 15);
+      if (m < M && n < N) {
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = apply_act(act, acc[i][j][q] * alpha + bv[q]);
+        Store4<TOut>::run(C + (int64_t)m * p.ldc, n, N, vec_ok, v);
+      }
+    }
+  }
+}
+
+}  // namespace sf

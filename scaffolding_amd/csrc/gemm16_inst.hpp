@@ -1,0 +1,79 @@
+// gemm16_inst.hpp — instantiation + launch table of the 16-bit GEMM for one
+// input type (included by gemm16_bf16.hip and gemm16_f16.hip).
+#pragma once
+
+#include "sf_internal.hpp"
+#include "skinny16.hpp"
+
+namespace sf {
+
+template <typename TIn, typename TOut, bool KM>
+static int launch16_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hipStream_t st) {
+  const dim3 g(gx, gy);
+  switch (cfg) {
+    case TILE_256x256:
+      hipLaunchKernelGGL((gemm16_kernel<TIn, TOut, 256, 256, 2, 4, KM, true>), g, dim3(512), 0, st, p);
+      break;
+    case TILE_256x128:
+      hipLaunchKernelGGL((gemm16_kernel<TIn, TOut, 256, 128, 4, 2, KM, true>), g, dim3(512), 0, st, p);
+      break;
+    case TILE_128x128:
+      hipLaunchKernelGGL((gemm16_kernel<TIn, TOut, 128, 128, 2, 2, KM, true>), g, dim3(256), 0, st, p);
+      break;
+    case TILE_256x64:
+      hipLaunchKernelGGL((gemm16_kernel<TIn, TOut, 256, 64, 4, 1, KM, true>), g, dim3(256), 0, st, p);
+      break;
+    case TILE_64x64:
+      hipLaunchKernelGGL((gemm16_kernel<TIn, TOut, 64, 64, 2, 2, KM, true>), g, dim3(256), 0, st, p);
+      break;
+    case TILE_GENERIC:
+      hipLaunchKernelGGL((gemm16_kernel<TIn, TOut, 64, 64, 2, 2, KM, false>), g, dim3(256), 0, st, p);
+      break;
+    case TILE_SKINNY:
+      if constexpr (KM) {
+        // grid.x = ceil(N / 32): 2 row blocks per workgroup, K split over 4 waves.
+        hipLaunchKernelGGL((skinny16_kernel<TIn, TOut, 4, 2, 8>), g, dim3(256), 0, st, p);
+        break;
+      }
+      return fail(SF_ERR_UNSUPPORTED, "skinny kernel needs a K-contiguous B");
+    default:
+      return fail(SF_ERR_INVALID_ARG, "unknown tile config %d", cfg);
+  }
+  return check_launch(tile_name(cfg));
+}
+
+// Only the tiles the dispatcher picks for an fp32 output of 16-bit inputs.
+template <typename TIn, bool KM>
+static int launch16_f32out(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hipStream_t st) {
+  const dim3 g(gx, gy);
+  switch (cfg) {
+    case TILE_128x128:
+      hipLaunchKernelGGL((gemm16_kernel<TIn, float, 128, 128, 2, 2, KM, true>), g, dim3(256), 0, st, p);
+      break;
+    case TILE_GENERIC:
+      hipLaunchKernelGGL((gemm16_kernel<TIn, float, 64, 64, 2, 2, KM, false>), g, dim3(256), 0, st, p);
+      break;
+    case TILE_SKINNY:
+      if constexpr (KM) {
+        hipLaunchKernelGGL((skinny16_kernel<TIn, float, 4, 2, 8>), g, dim3(256), 0, st, p);
+        break;
+      }
+      return fail(SF_ERR_UNSUPPORTED, "skinny kernel needs a K-contiguous B");
+    default:
+      return fail(SF_ERR_INVALID_ARG, "tile config %d has no fp32-output variant", cfg);
+  }
+  return check_launch(tile_name(cfg));
+}
+
+template <typename TIn>
+static int launch16_in(sf_dtype in, sf_dtype out, bool b_kmajor, int cfg, const GemmParams& p,
+                       unsigned gx, unsigned gy, hipStream_t st) {
+  if (out == SF_F32)
+    return b_kmajor ? launch16_f32out<TIn, true>(cfg, p, gx, gy, st)
+                    : launch16_f32out<TIn, false>(cfg, p, gx, gy, st);
+  (void)in;
+  return b_kmajor ? launch16_t<TIn, TIn, true>(cfg, p, gx, gy, st)
+                  : launch16_t<TIn, TIn, false>(cfg, p, gx, gy, st);
+}
+
+}  // namespace sf

@@ -1,0 +1,42 @@
+// gemm32.hip — fp32 GEMM instantiations and launcher.
+#include "gemm32.hpp"
+#include "sf_internal.hpp"
+
+namespace sf {
+
+template <bool KM>
+static int launch32_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hipStream_t st) {
+  const dim3 g(gx, gy);
+  switch (cfg) {
+    case TILE_128x128:
+      hipLaunchKernelGGL((gemm32_kernel<128, 128, 2, 2, KM, true>), g, dim3(256), 0, st, p);
+      break;
+    case TILE_64x64:
+      hipLaunchKernelGGL((gemm32_kernel<64, 64, 2, 2, KM, true>), g, dim3(256), 0, st, p);
+      break;
+    case TILE_GENERIC:
+      hipLaunchKernelGGL((gemm32_kernel<64, 64, 2, 2, KM, false>), g, dim3(256), 0, st, p);
+      break;
+    default:
+      return fail(SF_ERR_INVALID_ARG, "tile config %d has no fp32 variant", cfg);
+  }
+  return check_launch(tile_name(cfg));
+}
+
+int launch_gemm32(bool b_kmajor, int cfg, const GemmParams& p, int64_t batch, hipStream_t st) {
+  const unsigned gx = static_cast<unsigned>(p.tiles_m) * static_cast<unsigned>(p.tiles_n);
+  // grid.y is limited to 65535: walk the batch in chunks.
+  for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
+    const int64_t nb = (batch - b0) < 65535 ? (batch - b0) : 65535;
+    GemmParams q = p;
+    q.A = static_cast<const float*>(p.A) + b0 * p.sA;
+    q.B = static_cast<const float*>(p.B) + b0 * p.sB;
+    q.C = static_cast<float*>(p.C) + b0 * p.sC;
+    const int rc = b_kmajor ? launch32_t<true>(cfg, q, gx, static_cast<unsigned>(nb), st)
+                            : launch32_t<false>(cfg, q, gx, static_cast<unsigned>(nb), st);
+    if (rc != SF_OK) return rc;
+  }
+  return SF_OK;
+}
+
+}  // namespace sf

@@ -1,0 +1,305 @@
+// rowops.hip — HBM-bound row and elementwise kernels of the path:
+// row softmax (with the SDPA pre-scale folded in), standalone SiLU / GELU /
+// scalar-multiply / bias-add, dtype casts and a zero fill.
+#include "sf_internal.hpp"
+
+namespace sf {
+
+// Generic 8-element chunk load/store for any element type.  `vec` selects
+// the 16-byte (16-bit types) / 2x16-byte (fp32) path, else per element.
+template <typename T> struct Chunk8;
+template <> struct Chunk8<float> {
+  __device__ __forceinline__ static void load(const void* base, int64_t i, float v[8]) {
+    const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + i);
+    f32x4 a = p[0], b = p[1];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { v[e] = a[e]; v[e + 4] = b[e]; }
+  }
+  __device__ __forceinline__ static void store(void* base, int64_t i, const float v[8]) {
+    f32x4* p = reinterpret_cast<f32x4*>(static_cast<float*>(base) + i);
+    p[0] = f32x4{v[0], v[1], v[2], v[3]};
+    p[1] = f32x4{v[4], v[5], v[6], v[7]};
+  }
+  __device__ __forceinline__ static float get(const void* base, int64_t i) {
+    return static_cast<const float*>(base)[i];
+  }
+  __device__ __forceinline__ static void put(void* base, int64_t i, float v) {
+    static_cast<float*>(base)[i] = v;
+  }
+};
+template <typename T> struct Chunk8 {  // BF16 / F16
+  __device__ __forceinline__ static void load(const void* base, int64_t i, float v[8]) {
+    u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + i);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      v[e] = Elem<T>::to_f32(static_cast<uint16_t>(w[e >> 1] >> ((e & 1) * 16)));
+  }
+  __device__ __forceinline__ static void store(void* base, int64_t i, const float v[8]) {
+    u32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w[e] = static_cast<uint32_t>(Elem<T>::from_f32(v[2 * e])) |
+             (static_cast<uint32_t>(Elem<T>::from_f32(v[2 * e + 1])) << 16);
+    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + i) = w;
+  }
+  __device__ __forceinline__ static float get(const void* base, int64_t i) {
+    return Elem<T>::to_f32(static_cast<const uint16_t*>(base)[i]);
+  }
+  __device__ __forceinline__ static void put(void* base, int64_t i, float v) {
+    static_cast<uint16_t*>(base)[i] = Elem<T>::from_f32(v);
+  }
+};
+
+// ---------------------------------------------------------------------
+// Softmax, one wave per row, the row held in registers (CPL chunks of 8
+// elements per lane; cols <= 512 * CPL, cols % 8 == 0, rows 16-B aligned).
+// One HBM read and one write per element.
+// ---------------------------------------------------------------------
+template <typename TI, typename TO, int CPL>
+__global__ __launch_bounds__(256) void softmax_wave_kernel(const void* __restrict__ x,
+                                                           void* __restrict__ y, int64_t rows,
+                                                           int cols, float scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nch = cols >> 3;
+  const int64_t base = row * cols;
+  float v[CPL][8];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = c * 64 + lane;
+    if (ch < nch) {
+      Chunk8<TI>::load(x, base + ch * 8, v[c]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[c][e] *= scale;
+        mx = fmaxf(mx, v[c][e]);
+      }
+    }
+  }
+  mx = wave_max(mx);
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = c * 64 + lane;
+    if (ch < nch) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[c][e] = fast_exp(v[c][e] - mx);
+        s += v[c][e];
+      }
+    }
+  }
+  s = wave_sum(s);
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = c * 64 + lane;
+    if (ch < nch) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[c][e] *= inv;
+      Chunk8<TO>::store(y, base + ch * 8, v[c]);
+    }
+  }
+}
+
+// Any cols / alignment: one 256-thread block per row, three passes (max,
+// sum of exp, write) over the row; the re-reads hit L2 for rows that fit.
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void softmax_block_kernel(const void* __restrict__ x,
+                                                            void* __restrict__ y, int64_t rows,
+                                                            int64_t cols, float scale) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t base = row * cols;
+  float mx = -INFINITY;
+  for (int64_t c = tid; c < cols; c += 256) mx = fmaxf(mx, Chunk8<TI>::get(x, base + c) * scale);
+  mx = wave_max(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float s = 0.f;
+  for (int64_t c = tid; c < cols; c += 256) s += fast_exp(Chunk8<TI>::get(x, base + c) * scale - mx);
+  s = wave_sum(s);
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  s = red[0] + red[1] + red[2] + red[3];
+  const float inv = 1.0f / s;
+  for (int64_t c = tid; c < cols; c += 256)
+    Chunk8<TO>::put(y, base + c, fast_exp(Chunk8<TI>::get(x, base + c) * scale - mx) * inv);
+}
+
+// ---------------------------------------------------------------------
+// Elementwise: y = f(x) over n elements, 8 per thread per iteration.
+// ---------------------------------------------------------------------
+enum UnaryOp { U_SILU = 0, U_GELU = 1, U_MULS = 2 };
+
+template <typename T, int OP>
+__global__ __launch_bounds__(256) void unary_kernel(const void* x, void* y, int64_t n, float s,
+                                                    bool vec) {
+  const int64_t stride = (int64_t)gridDim.x * 256 * 8;
+  for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8; i < n; i += stride) {
+    float v[8];
+    const bool full = vec && i + 8 <= n;
+    if (full) {
+      Chunk8<T>::load(x, i, v);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (i + e < n) ? Chunk8<T>::get(x, i + e) : 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (OP == U_SILU) v[e] = silu_f32(v[e]);
+      else if (OP == U_GELU) v[e] = gelu_tanh_f32(v[e]);
+      else v[e] = v[e] * s;
+    }
+    if (full) {
+      Chunk8<T>::store(y, i, v);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (i + e < n) Chunk8<T>::put(y, i + e, v[e]);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void bias_rows_kernel(void* C, const void* bias, int64_t M,
+                                                        int64_t N) {
+  const int64_t total = M * N;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += stride) {
+    float v = Chunk8<T>::get(C, i) + Chunk8<T>::get(bias, i % N);
+    Chunk8<T>::put(C, i, v);
+  }
+}
+
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void cast_kernel(const void* x, void* y, int64_t n, bool vec) {
+  const int64_t stride = (int64_t)gridDim.x * 256 * 8;
+  for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8; i < n; i += stride) {
+    float v[8];
+    if (vec && i + 8 <= n) {
+      Chunk8<TI>::load(x, i, v);
+      Chunk8<TO>::store(y, i, v);
+    } else {
+      for (int e = 0; e < 8 && i + e < n; ++e) Chunk8<TO>::put(y, i + e, Chunk8<TI>::get(x, i + e));
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void zero_kernel(uint8_t* p, size_t nbytes) {
+  // Head bytes up to 16-B alignment, 16-B body, tail bytes.
+  const size_t head = (16 - (reinterpret_cast<uintptr_t>(p) & 15)) & 15;
+  const size_t h = head < nbytes ? head : nbytes;
+  const size_t body = (nbytes - h) / 16;
+  const size_t tid = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t stride = (size_t)gridDim.x * 256;
+  if (tid < h) p[tid] = 0;
+  u32x4* q = reinterpret_cast<u32x4*>(p + h);
+  for (size_t i = tid; i < body; i += stride) q[i] = u32x4{0u, 0u, 0u, 0u};
+  const size_t tail0 = h + body * 16;
+  if (tid < nbytes - tail0) p[tail0 + tid] = 0;
+}
+
+// ---------------------------------------------------------------------
+// Launchers
+// ---------------------------------------------------------------------
+static unsigned grid_for(int64_t work_items) {
+  int64_t g = (work_items + 255) / 256;
+  if (g < 1) g = 1;
+  if (g > 8192) g = 8192;  // grid-stride beyond 32 blocks per CU
+  return static_cast<unsigned>(g);
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+template <typename TI, typename TO>
+static void softmax_launch_t(const void* x, void* y, int64_t rows, int64_t cols, float scale,
+                             hipStream_t st) {
+  const bool vec = (cols % 8 == 0) && aligned16(x) && aligned16(y) && cols <= 8192;
+  if (vec) {
+    const unsigned grid = static_cast<unsigned>((rows + 3) / 4);
+    const int c = static_cast<int>(cols);
+    if (cols <= 512)
+      hipLaunchKernelGGL((softmax_wave_kernel<TI, TO, 1>), dim3(grid), dim3(256), 0, st, x, y, rows, c, scale);
+    else if (cols <= 1024)
+      hipLaunchKernelGGL((softmax_wave_kernel<TI, TO, 2>), dim3(grid), dim3(256), 0, st, x, y, rows, c, scale);
+    else if (cols <= 2048)
+      hipLaunchKernelGGL((softmax_wave_kernel<TI, TO, 4>), dim3(grid), dim3(256), 0, st, x, y, rows, c, scale);
+    else if (cols <= 4096)
+      hipLaunchKernelGGL((softmax_wave_kernel<TI, TO, 8>), dim3(grid), dim3(256), 0, st, x, y, rows, c, scale);
+    else
+      hipLaunchKernelGGL((softmax_wave_kernel<TI, TO, 16>), dim3(grid), dim3(256), 0, st, x, y, rows, c, scale);
+  } else {
+    hipLaunchKernelGGL((softmax_block_kernel<TI, TO>), dim3(static_cast<unsigned>(rows)), dim3(256), 0,
+                       st, x, y, rows, cols, scale);
+  }
+}
+
+template <typename TI>
+static void softmax_launch_i(sf_dtype out, const void* x, void* y, int64_t rows, int64_t cols,
+                             float scale, hipStream_t st) {
+  if (out == SF_F32) softmax_launch_t<TI, float>(x, y, rows, cols, scale, st);
+  else if (out == SF_F16) softmax_launch_t<TI, F16>(x, y, rows, cols, scale, st);
+  else softmax_launch_t<TI, BF16>(x, y, rows, cols, scale, st);
+}
+
+int launch_softmax(const void* x, void* y, int64_t rows, int64_t cols, sf_dtype in, sf_dtype out,
+                   float scale, hipStream_t st) {
+  if (in == SF_F32) softmax_launch_i<float>(out, x, y, rows, cols, scale, st);
+  else if (in == SF_F16) softmax_launch_i<F16>(out, x, y, rows, cols, scale, st);
+  else softmax_launch_i<BF16>(out, x, y, rows, cols, scale, st);
+  return check_launch("softmax");
+}
+
+template <typename T>
+static void unary_launch_t(int op, const void* x, void* y, int64_t n, float s, hipStream_t st) {
+  const bool vec = aligned16(x) && aligned16(y);
+  const unsigned grid = grid_for((n + 7) / 8);
+  if (op == U_SILU) hipLaunchKernelGGL((unary_kernel<T, U_SILU>), dim3(grid), dim3(256), 0, st, x, y, n, s, vec);
+  else if (op == U_GELU) hipLaunchKernelGGL((unary_kernel<T, U_GELU>), dim3(grid), dim3(256), 0, st, x, y, n, s, vec);
+  else hipLaunchKernelGGL((unary_kernel<T, U_MULS>), dim3(grid), dim3(256), 0, st, x, y, n, s, vec);
+}
+
+int launch_unary(int op, const void* x, void* y, int64_t n, sf_dtype dt, float s, hipStream_t st) {
+  if (dt == SF_F32) unary_launch_t<float>(op, x, y, n, s, st);
+  else if (dt == SF_F16) unary_launch_t<F16>(op, x, y, n, s, st);
+  else unary_launch_t<BF16>(op, x, y, n, s, st);
+  return check_launch("elementwise");
+}
+
+int launch_bias_rows(void* C, const void* bias, int64_t M, int64_t N, sf_dtype dt, hipStream_t st) {
+  const unsigned grid = grid_for(M * N);
+  if (dt == SF_F32) hipLaunchKernelGGL((bias_rows_kernel<float>), dim3(grid), dim3(256), 0, st, C, bias, M, N);
+  else if (dt == SF_F16) hipLaunchKernelGGL((bias_rows_kernel<F16>), dim3(grid), dim3(256), 0, st, C, bias, M, N);
+  else hipLaunchKernelGGL((bias_rows_kernel<BF16>), dim3(grid), dim3(256), 0, st, C, bias, M, N);
+  return check_launch("bias_add_rows");
+}
+
+template <typename TI>
+static void cast_launch_i(sf_dtype out, const void* x, void* y, int64_t n, hipStream_t st) {
+  const bool vec = aligned16(x) && aligned16(y);
+  const unsigned grid = grid_for((n + 7) / 8);
+  if (out == SF_F32) hipLaunchKernelGGL((cast_kernel<TI, float>), dim3(grid), dim3(256), 0, st, x, y, n, vec);
+  else if (out == SF_F16) hipLaunchKernelGGL((cast_kernel<TI, F16>), dim3(grid), dim3(256), 0, st, x, y, n, vec);
+  else hipLaunchKernelGGL((cast_kernel<TI, BF16>), dim3(grid), dim3(256), 0, st, x, y, n, vec);
+}
+
+int launch_cast(const void* x, sf_dtype in, void* y, sf_dtype out, int64_t n, hipStream_t st) {
+  if (in == SF_F32) cast_launch_i<float>(out, x, y, n, st);
+  else if (in == SF_F16) cast_launch_i<F16>(out, x, y, n, st);
+  else cast_launch_i<BF16>(out, x, y, n, st);
+  return check_launch("cast");
+}
+
+int launch_zero(void* p, size_t nbytes, hipStream_t st) {
+  const unsigned grid = grid_for(static_cast<int64_t>((nbytes + 15) / 16));
+  hipLaunchKernelGGL(zero_kernel, dim3(grid), dim3(256), 0, st, static_cast<uint8_t*>(p), nbytes);
+  return check_launch("zero");
+}
+
+}  // namespace sf

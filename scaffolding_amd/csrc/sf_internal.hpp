@@ -1,0 +1,50 @@
+// sf_internal.hpp — host-side declarations shared by the translation units
+// of libsfgemm (launchers, error reporting).  Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "gemm16.hpp"
+#include "sf_common.hpp"
+
+namespace sf {
+
+// Records a formatted message as this thread's last error; returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Maps a pending launch error (hipGetLastError) to SF_ERR_HIP with context.
+int check_launch(const char* what);
+// Maps a HIP status to SF_OK / SF_ERR_HIP with context.
+int check_hip(hipError_t e, const char* what);
+
+// Tile shapes of the 16-bit and fp32 GEMM kernels.
+enum TileCfg {
+  TILE_256x256 = 0,  // 512 threads, waves 2x4 of 128x64
+  TILE_256x128 = 1,  // 512 threads, waves 4x2 of 64x64
+  TILE_128x128 = 2,  // 256 threads, waves 2x2 of 64x64
+  TILE_256x64 = 3,   // 256 threads, waves 4x1 of 64x64 (narrow N, e.g. P.V)
+  TILE_64x64 = 4,    // 256 threads, waves 2x2 of 32x32
+  TILE_GENERIC = 5,  // 64x64, element-wise bounds-checked loads (any layout)
+  TILE_SKINNY = 6    // M <= 16 stream kernel
+};
+const char* tile_name(int cfg);
+
+// One GEMM launch: batch entries [0, batch) of p, grid.y <= 65535 per call.
+int launch_gemm16(sf_dtype in, sf_dtype out, bool b_kmajor, int cfg, const GemmParams& p,
+                  int64_t batch, hipStream_t st);
+int launch_gemm16_bf16(sf_dtype out, bool b_kmajor, int cfg, const GemmParams& p, unsigned gx,
+                       unsigned gy, hipStream_t st);
+int launch_gemm16_f16(sf_dtype out, bool b_kmajor, int cfg, const GemmParams& p, unsigned gx,
+                      unsigned gy, hipStream_t st);
+int launch_gemm32(bool b_kmajor, int cfg, const GemmParams& p, int64_t batch, hipStream_t st);
+
+// Tile edge of a config (BM, BN).
+void tile_dims(int cfg, bool fp32, int& bm, int& bn);
+
+int launch_softmax(const void* x, void* y, int64_t rows, int64_t cols, sf_dtype in, sf_dtype out,
+                   float scale, hipStream_t st);
+int launch_unary(int op, const void* x, void* y, int64_t n, sf_dtype dt, float s, hipStream_t st);
+int launch_bias_rows(void* C, const void* bias, int64_t M, int64_t N, sf_dtype dt, hipStream_t st);
+int launch_cast(const void* x, sf_dtype in, void* y, sf_dtype out, int64_t n, hipStream_t st);
+int launch_zero(void* p, size_t nbytes, hipStream_t st);
+
+}  // namespace sf

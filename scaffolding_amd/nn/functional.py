@@ -1,0 +1,59 @@
+"""Functional ops of the path (reference nn/functional.py).
+
+  linear                          reference nn/functional.py:374-395
+  silu / gelu (tanh)              reference nn/functional.py:37-89
+  softmax                         reference nn/functional.py:113-145
+  scaled_dot_product_attention    reference nn/functional.py:298-369
+
+GPU only; results carry no grad_fn (as the reference's GPU branches).
+"""
+from __future__ import annotations
+
+import math
+
+from .. import _cuda_ops as _cuops
+from ..tensor import Tensor, _gpu_only
+from .layers import _linear
+
+
+def linear(input: Tensor, weight: Tensor, bias: Tensor | None = None,
+           activation: str | None = None) -> Tensor:
+    return _linear(input, weight, bias, activation)
+
+
+def silu(input: Tensor) -> Tensor:
+    if input._gpu is None:
+        _gpu_only("silu")
+    return Tensor._wrap_gpu(_cuops.dev_silu(input._gpu), input._device)
+
+
+def gelu(input: Tensor, approximate: str = "tanh") -> Tensor:
+    if input._gpu is None:
+        _gpu_only("gelu")
+    if approximate != "tanh":
+        raise NotImplementedError("only the tanh approximation is on the device path")
+    return Tensor._wrap_gpu(_cuops.dev_gelu(input._gpu), input._device)
+
+
+def softmax(input: Tensor, dim: int = -1, dtype=None) -> Tensor:
+    if input._gpu is None:
+        _gpu_only("softmax")
+    if dtype is not None:
+        raise NotImplementedError("softmax(dtype=...) is not on the device path")
+    return Tensor._wrap_gpu(_cuops.dev_softmax(input._gpu, dim), input._device)
+
+
+def scaled_dot_product_attention(q: Tensor, k: Tensor, v: Tensor, attn_mask=None,
+                                 dropout_p: float = 0.0, scale: float | None = None) -> Tensor:
+    """softmax(scale * q k^T) v: one strided-batched QK^T launch with the
+    scale in its epilogue, one row softmax, one strided-batched PV launch.
+    The reference's GPU path (nn/functional.py:310-321) runs a Python loop
+    of per-head SGEMMs, a scale pass, the softmax and a batched SGEMM."""
+    if q._gpu is None or k._gpu is None or v._gpu is None:
+        _gpu_only("scaled_dot_product_attention")
+    if attn_mask is not None or dropout_p > 0.0:
+        raise NotImplementedError("attn_mask / dropout are not on the device path")
+    d = q.shape[-1]
+    s = (1.0 / math.sqrt(d)) if scale is None else float(scale)
+    out = _cuops.dev_scaled_dot_product_attention(q._gpu, k._gpu, v._gpu, s)
+    return Tensor._wrap_gpu(out, q._device)

@@ -1,0 +1,208 @@
+"""GEMM parity on the GPU, small and ragged shapes: every tile config and
+operand layout of sf_gemm against the fp64 closed form (and, for fp32,
+against the reference's CPU fp32 path), through the Cython seam and the C
+ABI."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import check_bound, cu, down, gemm_bound, quantize, ref, rnd, up
+from oracle.configs import normwise_err, tol_fp32
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = ["float32", "float16", "bfloat16"]
+
+
+def _case(rng, m, n, k, dtype, nt):
+    a = rnd(rng, (m, k), 1.0, dtype)
+    b = rnd(rng, (n, k) if nt else (k, n), 1.0 / np.sqrt(max(k, 1)), dtype)
+    return a, b
+
+
+def test_sgemm_known_answer_like_reference():
+    """Mirror of the reference's only GEMM known-answer check
+    (tests/test_mps_ops.py:24-33): seed 42, 3x4 @ 4x2, max error < 1e-5
+    against NumPy."""
+    np.random.seed(42)
+    a = np.random.randn(3, 4).astype(np.float32)
+    b = np.random.randn(4, 2).astype(np.float32)
+    c = down(cu().dev_matmul(up(a, "float32"), up(b, "float32")))
+    assert c.shape == (3, 2)
+    assert np.max(np.abs(c - a @ b)) < 1e-5
+
+
+SMALL = [(1, 1, 1), (3, 5, 7), (2, 3, 8), (5, 9, 16), (17, 33, 65), (64, 64, 64),
+         (100, 130, 72), (129, 257, 200), (16, 48, 4096), (33, 40, 96), (7, 300, 1000),
+         (255, 257, 128), (300, 64, 520)]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("nt", [False, True], ids=["NN", "NT"])
+@pytest.mark.parametrize("shape", SMALL, ids=lambda s: "x".join(map(str, s)))
+def test_gemm_small(dtype, nt, shape):
+    m, n, k = shape
+    rng = np.random.default_rng(1000 + m * 7 + n * 13 + k)
+    a, b = _case(rng, m, n, k, dtype, nt)
+    ga, gb = up(a, dtype), up(b, dtype)
+    y = down(cu().dev_matmul_nt(ga, gb) if nt else cu().dev_matmul(ga, gb))
+    bm = b.T if nt else b
+    y64 = ref.matmul_f64(a, bm)
+    absprod = np.abs(a.astype(np.float64)) @ np.abs(bm.astype(np.float64))
+    assert y.shape == (m, n)
+    check_bound(y, y64, gemm_bound(y64, absprod, k, dtype), "%s %s %s" % (dtype, nt, shape))
+    if dtype == "float32":
+        y_cpu = ref.matmul_nt(a, b) if nt else ref.matmul(a, b)
+        assert normwise_err(y, y_cpu) <= tol_fp32(k)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("act", [None, "silu", "gelu"])
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("shape", [(1, 40, 64), (16, 1000, 256), (3, 17, 24), (70, 200, 136),
+                                   (300, 520, 264)], ids=lambda s: "x".join(map(str, s)))
+def test_linear_epilogues(dtype, act, bias, shape):
+    m, n, k = shape
+    rng = np.random.default_rng(77 + m + n + k)
+    x = rnd(rng, (m, k), 1.0, dtype)
+    w = rnd(rng, (n, k), 1.0 / np.sqrt(k), dtype)
+    b = rnd(rng, (n,), 0.5, dtype) if bias else None
+    gb = up(b, dtype) if bias else None
+    y = down(cu().dev_linear_forward(up(x, dtype), up(w, dtype), gb, act))
+    y64 = ref.linear_f64(x, w, b, act)
+    absprod = np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+    check_bound(y, y64, gemm_bound(y64, absprod, k, dtype, act), "linear %s %s %s" % (dtype, act, shape))
+
+
+def test_linear_leading_dims_and_strides():
+    """Output shape x.shape[:-1] + (N,), C-contiguous (reference
+    _cuda_ops.pyx:1301)."""
+    rng = np.random.default_rng(5)
+    x = rnd(rng, (2, 3, 5, 64), 1.0, "bfloat16")
+    w = rnd(rng, (24, 64), 0.1, "bfloat16")
+    gy = cu().dev_linear_forward(up(x, "bfloat16"), up(w, "bfloat16"))
+    assert gy.shape == (2, 3, 5, 24)
+    y = down(gy)
+    assert y.flags.c_contiguous and y.strides == (3 * 5 * 24 * 4, 5 * 24 * 4, 24 * 4, 4)
+    y64 = ref.linear_f64(x.reshape(-1, 64), w).reshape(2, 3, 5, 24)
+    absprod = (np.abs(x.reshape(-1, 64).astype(np.float64)) @ np.abs(w.astype(np.float64)).T).reshape(y64.shape)
+    check_bound(y, y64, gemm_bound(y64, absprod, 64, "bfloat16"))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("nt", [False, True], ids=["NN", "NT"])
+@pytest.mark.parametrize("bcast", ["none", "b2d", "a2d"])
+def test_batched(dtype, nt, bcast):
+    rng = np.random.default_rng(11)
+    bshape, m, n, k = (2, 3), 40, 72, 48
+    a_shape = (m, k) if bcast == "a2d" else bshape + (m, k)
+    b_core = (n, k) if nt else (k, n)
+    b_shape = b_core if bcast == "b2d" else bshape + b_core
+    a = rnd(rng, a_shape, 1.0, dtype)
+    b = rnd(rng, b_shape, 1.0 / np.sqrt(k), dtype)
+    fn = cu().dev_batched_matmul_nt if nt else cu().dev_batched_matmul
+    y = down(fn(up(a, dtype), up(b, dtype)))
+    bm = np.swapaxes(b, -2, -1) if nt else b
+    y64 = np.matmul(a.astype(np.float64), bm.astype(np.float64))
+    absprod = np.matmul(np.abs(a.astype(np.float64)), np.abs(bm.astype(np.float64)))
+    assert y.shape == bshape + (m, n)
+    check_bound(y, y64, gemm_bound(y64, absprod, k, dtype), "batched %s %s %s" % (dtype, nt, bcast))
+
+
+def test_batched_nt_alpha():
+    rng = np.random.default_rng(12)
+    q = rnd(rng, (4, 96, 64), 1.0, "float16")
+    k = rnd(rng, (4, 80, 64), 1.0, "float16")
+    s = down(cu().dev_batched_matmul_nt(up(q, "float16"), up(k, "float16"), 0.125))
+    s64 = 0.125 * np.matmul(q.astype(np.float64), np.swapaxes(k, -2, -1).astype(np.float64))
+    absprod = 0.125 * np.matmul(np.abs(q.astype(np.float64)), np.abs(np.swapaxes(k, -2, -1)).astype(np.float64))
+    check_bound(s, s64, gemm_bound(s64, absprod, 64, "float16"))
+
+
+# Shapes chosen so the dispatcher picks each tile config (asserted through
+# sf_gemm_plan), checked on sampled rows plus row/column checksums.
+TILE_CASES = [
+    # (dtype, nt, M, N, K, batch, expected kernel)
+    ("bfloat16", True, 4096, 4096, 192, 1, "gemm tile 256x256"),
+    ("bfloat16", False, 4096, 4096, 192, 1, "gemm tile 256x256"),
+    ("float16", True, 2048, 4096, 136, 1, "gemm tile 256x128"),
+    ("bfloat16", False, 2048, 4096, 136, 1, "gemm tile 256x128"),
+    ("bfloat16", True, 2048, 2048, 200, 1, "gemm tile 128x128"),
+    ("float16", False, 2048, 2048, 200, 1, "gemm tile 128x128"),
+    ("float16", False, 4096, 64, 264, 16, "gemm tile 256x64"),
+    ("bfloat16", True, 4096, 48, 264, 16, "gemm tile 256x64"),
+    ("bfloat16", True, 300, 500, 256, 1, "gemm tile 64x64"),
+    ("float16", True, 300, 500, 250, 1, "gemm tile generic"),
+    ("bfloat16", False, 300, 500, 250, 1, "gemm tile generic"),
+    ("bfloat16", True, 16, 11008, 4096, 1, "gemm skinny"),
+    ("float16", True, 5, 333, 1000, 3, "gemm skinny"),
+    ("float32", True, 2048, 2048, 136, 1, "gemm tile 128x128"),
+    ("float32", False, 2048, 2048, 136, 1, "gemm tile 128x128"),
+    ("float32", False, 1000, 900, 100, 1, "gemm tile 64x64"),
+    ("float32", True, 333, 270, 99, 1, "gemm tile generic"),
+]
+
+
+@pytest.mark.parametrize("case", TILE_CASES, ids=lambda c: "%s-%s-%dx%dx%dx%d" % (c[0], "NT" if c[1] else "NN", c[2], c[3], c[4], c[5]))
+def test_tile_configs(case):
+    dtype, nt, m, n, k, batch, expect = case
+    rng = np.random.default_rng(m + 3 * n + 5 * k + batch)
+    shp = lambda *s: ((batch,) if batch > 1 else ()) + s  # noqa: E731
+    a = rnd(rng, shp(m, k), 1.0, dtype)
+    b = rnd(rng, shp(n, k) if nt else shp(k, n), 1.0 / np.sqrt(k), dtype)
+    ga, gb = up(a, dtype), up(b, dtype)
+    ldb = k if nt else n
+    plan = cu().gemm_plan(1 if nt else 0, m, n, k, batch, ga.data_ptr, k, m * k if batch > 1 else 0,
+                          gb.data_ptr, ldb, n * k if batch > 1 else 0, n, m * n, ga.dtype)
+    assert plan.startswith(expect), plan
+    if batch > 1:
+        fn = cu().dev_batched_matmul_nt if nt else cu().dev_batched_matmul
+    else:
+        fn = cu().dev_matmul_nt if nt else cu().dev_matmul
+    y = down(fn(ga, gb)).reshape(batch, m, n)
+    a3 = a.reshape(batch, m, k).astype(np.float64)
+    b3 = b.reshape((batch, n, k) if nt else (batch, k, n)).astype(np.float64)
+    bm = np.swapaxes(b3, -2, -1) if nt else b3
+    rows = np.unique(np.r_[0, m - 1, np.arange(0, m, 97), np.arange(255, m, 256), np.arange(256, m, 256)])
+    for bi in sorted({0, batch - 1}):
+        y64 = a3[bi, rows] @ bm[bi]
+        absprod = np.abs(a3[bi, rows]) @ np.abs(bm[bi])
+        check_bound(y[bi, rows], y64, gemm_bound(y64, absprod, k, dtype), "%s rows" % (case,))
+        # Checksums over every row and column of this batch entry.
+        rs = y[bi].astype(np.float64).sum(axis=1)
+        rs64 = a3[bi] @ bm[bi].sum(axis=1)
+        cs = y[bi].astype(np.float64).sum(axis=0)
+        cs64 = a3[bi].sum(axis=0) @ bm[bi]
+        full_abs = np.abs(a3[bi]) @ np.abs(bm[bi])
+        eps = 2 * (k * 2.0 ** -23 + {"float32": 2.0 ** -24, "float16": 2.0 ** -11, "bfloat16": 2.0 ** -8}[dtype])
+        assert np.all(np.abs(rs - rs64) <= eps * full_abs.sum(axis=1) + 1e-6), "row checksum %s" % (case,)
+        assert np.all(np.abs(cs - cs64) <= eps * full_abs.sum(axis=0) + 1e-6), "col checksum %s" % (case,)
+
+
+def test_k_zero_writes_epilogue_of_zero():
+    x = np.zeros((5, 0), np.float32)
+    w = np.zeros((7, 0), np.float32)
+    b = np.linspace(-1, 1, 7).astype(np.float32)
+    y = down(cu().dev_linear_forward(up(x, "float32"), up(w, "float32"), up(b, "float32"), "silu"))
+    np.testing.assert_allclose(y, np.broadcast_to(ref.silu(b.astype(np.float64)), (5, 7)), rtol=1e-6, atol=1e-7)
+
+
+def test_empty_outputs():
+    g = cu()
+    y = g.dev_matmul(up(np.zeros((0, 4), np.float32), "float32"), up(np.zeros((4, 3), np.float32), "float32"))
+    assert y.shape == (0, 3)
+    y = g.dev_linear_forward(up(np.zeros((4, 8), np.float32), "bfloat16"), up(np.zeros((0, 8), np.float32), "bfloat16"))
+    assert y.shape == (4, 0)
+
+
+def test_shape_errors():
+    g = cu()
+    a = up(np.zeros((4, 8), np.float32), "float32")
+    b = up(np.zeros((9, 3), np.float32), "float32")
+    with pytest.raises(ValueError):
+        g.dev_matmul(a, b)
+    with pytest.raises(TypeError):
+        g.dev_matmul(a, up(np.zeros((8, 3), np.float32), "bfloat16"))
+    with pytest.raises(ValueError):
+        g.dev_linear_forward(a, up(np.zeros((3, 7), np.float32), "float32"))
