@@ -1,0 +1,303 @@
+#!/usr/bin/env python3
+"""Benchmark of the matmul hot path on one MI355X.
+
+Headline (``value``): the north-star workload of BASELINE.json — bf16
+``linear_forward`` (GEMM + bias epilogue, fp32 accumulate) at
+M = N = K = 4096 — in TFLOP/s.  A "step" is one ``dev_linear_forward``
+launch over one resident 4096 x 4096 activation; K steps are timed with HIP
+events on the launch stream, bracketed by device synchronisation.
+
+``sweep`` times every other config of BASELINE.json the same way (C1 fp32
+Linear, C2 fp32 square matmul, C3 bf16 Linear+bias+SiLU at M = 1 / 16 /
+4096, C4 fp16 attention QK^T / softmax / PV, C5 bf16 DiT projections), with
+TFLOP/s or HBM GB/s and the roofline fraction.  HBM-bound skinny rows rotate
+four weight copies (> the 256 MB Infinity Cache) across steps.
+
+``cpu_baseline`` times the reference's Linux CPU path for the headline
+workload (NumPy fp32 ``x @ W.T + b``, reference nn/layers.py:129-131) on the
+host's BLAS threads, GC off, 1 warm-up, median of a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep]
+                       [--no-cpu] [--only NAME]
+"""
+from __future__ import annotations
+
+import argparse
+import gc
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "GEMM TFLOP/s & % MFMA peak (bf16/fp32 linear); skinny GEMM HBM GB/s"
+PEAK_BF16 = 2.5e15      # dense bf16/fp16 MFMA, FLOP/s
+PEAK_FP32 = 157.3e12    # fp32 matrix, FLOP/s
+PEAK_HBM = 8.0e12       # HBM3E, B/s
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gemm16_256x256_linear_4096.txt")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Dev:
+    """Synthetic resident inputs and event timing on the default stream."""
+
+    def __init__(self):
+        import scaffolding_amd as sf
+        self.sf = sf
+        self.cu = sf._cuops
+        self.rng = np.random.default_rng(1234)
+
+    def rand(self, shape, std, dtype):
+        # Host float32 normal draws, rounded to `dtype` by the device cast.
+        a = (self.rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
+        return self.cu.gputensor_from_numpy(a, 0, dtype)
+
+    def time_steps(self, fn, steps, warmup):
+        """Mean ms per call of fn over `steps` calls enqueued back to back
+        between two events (after `warmup` calls and a device sync)."""
+        cu = self.cu
+        for _ in range(warmup):
+            fn(0)
+        cu.device_synchronize()
+        e0, e1 = cu.CudaEvent(), cu.CudaEvent()
+        keep = []
+        e0.record()
+        for i in range(steps):
+            keep.append(fn(i))
+            if len(keep) > 8:
+                keep.pop(0)
+        e1.record()
+        e1.synchronize()
+        cu.device_synchronize()
+        return e0.elapsed_time(e1) / steps
+
+
+def headline(d: Dev, steps: int, warmup: int):
+    cu = d.cu
+    m = n = k = 4096
+    x = d.rand((m, k), 1.0, "bfloat16")
+    w = d.rand((n, k), 0.02, "bfloat16")
+    b = d.rand((n,), 0.01, "bfloat16")
+    kern = cu.gemm_plan(1, m, n, k, 1, x.data_ptr, k, 0, w.data_ptr, k, 0, n, 0, x.dtype,
+                        epi=1, ptr_bias=b.data_ptr)
+    ms = d.time_steps(lambda i: cu.dev_linear_forward(x, w, b), steps, warmup)
+    flops = 2.0 * m * n * k
+    return {"ms": ms, "flops": flops, "kernel": kern, "m": m, "n": n, "k": k,
+            "bytes": float((m * k + n * k + m * n) * 2 + n * 2)}
+
+
+def sweep(d: Dev, steps: int, warmup: int, only: str | None):
+    cu = d.cu
+    out = {}
+
+    def want(name):
+        return only is None or only in name
+
+    def rec(name, ms, flops, nbytes, bound, peak_flops):
+        t = ms * 1e-3
+        tf = flops / t
+        bw = nbytes / t
+        r = {"ms": round(ms, 5), "tflops": round(tf / 1e12, 2), "gbps": round(bw / 1e9, 1)}
+        if bound == "hbm":
+            r["roofline"] = {"bound": "hbm", "frac": round(bw / PEAK_HBM, 4)}
+        else:
+            r["roofline"] = {"bound": "mfma", "frac": round(tf / peak_flops, 4)}
+        out[name] = r
+        log("  %-34s %9.4f ms  %8.2f TFLOP/s  %8.1f GB/s  %s %.1f%%" % (
+            name, ms, tf / 1e12, bw / 1e9, bound, 100 * r["roofline"]["frac"]))
+
+    # C1: fp32 nn.Linear 64x512 -> 512 (+b); launch-latency bound, report time.
+    if want("C1"):
+        x = d.rand((64, 512), 1.0 / np.sqrt(512), np.float32)
+        w = d.rand((512, 512), 1.0 / np.sqrt(512), np.float32)
+        b = d.rand((512,), 0.05, np.float32)
+        ms = d.time_steps(lambda i: cu.dev_linear_forward(x, w, b), steps * 4, warmup)
+        rec("C1_fp32_linear_64x512x512", ms, 2.0 * 64 * 512 * 512,
+            (64 * 512 + 512 * 512 + 64 * 512 + 512) * 4.0, "mfma", PEAK_FP32)
+
+    # C2: fp32 square matmul.
+    for nn_ in (1024, 2048, 4096):
+        if not want("C2_fp32_matmul_%d" % nn_):
+            continue
+        a = d.rand((nn_, nn_), 0.5, np.float32)
+        bb = d.rand((nn_, nn_), 0.5, np.float32)
+        ms = d.time_steps(lambda i: cu.dev_matmul(a, bb), max(5, steps // (nn_ // 1024)), warmup)
+        rec("C2_fp32_matmul_%d" % nn_, ms, 2.0 * nn_ ** 3, 3.0 * nn_ * nn_ * 4, "mfma", PEAK_FP32)
+
+    # C3: bf16 Linear + bias + SiLU, K 4096 -> N 11008.
+    for m in (1, 16, 4096):
+        name = "C3_bf16_linear_silu_M%d" % m
+        if not want(name):
+            continue
+        k, n = 4096, 11008
+        x = d.rand((m, k), 1.0, "bfloat16")
+        copies = 4 if m <= 16 else 1
+        ws = [d.rand((n, k), 0.02, "bfloat16") for _ in range(copies)]
+        b = d.rand((n,), 0.01, "bfloat16")
+        ms = d.time_steps(lambda i: cu.dev_linear_forward(x, ws[i % copies], b, "silu"), steps, warmup)
+        nbytes = (m * k + n * k + m * n) * 2.0 + n * 2
+        rec(name, ms, 2.0 * m * n * k, nbytes, "hbm" if m <= 16 else "mfma", PEAK_BF16)
+        del ws
+
+    # C4: fp16 attention, 60 heads x 4096 x 64.
+    if want("C4"):
+        bh, s, dd = 60, 4096, 64
+        q = d.rand((bh, s, dd), 1.0, np.float16)
+        kk = d.rand((bh, s, dd), 1.0, np.float16)
+        v = d.rand((bh, s, dd), 1.0, np.float16)
+        st = max(3, steps // 10)
+        ms = d.time_steps(lambda i: cu.dev_batched_matmul_nt(q, kk, 0.125), st, 2)
+        rec("C4_fp16_qkT_scaled", ms, 2.0 * bh * s * s * dd, bh * (2 * s * dd + s * s) * 2.0, "hbm", PEAK_BF16)
+        scores = cu.dev_batched_matmul_nt(q, kk, 0.125)
+        ms = d.time_steps(lambda i: cu.dev_softmax(scores, -1), st, 2)
+        rec("C4_fp16_softmax", ms, 0.0, bh * s * s * 2 * 2.0, "hbm", PEAK_BF16)
+        probs = cu.dev_softmax(scores, -1)
+        del scores
+        ms = d.time_steps(lambda i: cu.dev_batched_matmul(probs, v), st, 2)
+        rec("C4_fp16_pv", ms, 2.0 * bh * s * s * dd, bh * (s * s + 2 * s * dd) * 2.0, "hbm", PEAK_BF16)
+        del probs
+        ms = d.time_steps(lambda i: cu.dev_scaled_dot_product_attention(q, kk, v, 0.125), st, 1)
+        rec("C4_fp16_sdpa_3kernel", ms, 4.0 * bh * s * s * dd, bh * (4 * s * dd + 4 * s * s) * 2.0, "hbm",
+            PEAK_BF16)
+
+    # C5: bf16 DiT projections, 17776 tokens.
+    tokens = 13 * (60 * 90 // 4) + 226
+    for pname, (k, n, has_b, act) in {"qkv": (1920, 5760, False, None), "out": (1920, 1920, True, None),
+                                      "mlp_up": (1920, 7680, True, "gelu"),
+                                      "mlp_down": (7680, 1920, True, None)}.items():
+        name = "C5_bf16_%s" % pname
+        if not want(name):
+            continue
+        x = d.rand((tokens, k), 1.0, "bfloat16")
+        w = d.rand((n, k), 0.02, "bfloat16")
+        b = d.rand((n,), 0.01, "bfloat16") if has_b else None
+        ms = d.time_steps(lambda i: cu.dev_linear_forward(x, w, b, act), steps, warmup)
+        rec(name, ms, 2.0 * tokens * n * k, (tokens * k + n * k + tokens * n) * 2.0, "mfma", PEAK_BF16)
+        del x, w
+
+    # Headline variant with the SiLU epilogue fused.
+    if want("north_star_bias_silu"):
+        x = d.rand((4096, 4096), 1.0, "bfloat16")
+        w = d.rand((4096, 4096), 0.02, "bfloat16")
+        b = d.rand((4096,), 0.01, "bfloat16")
+        ms = d.time_steps(lambda i: cu.dev_linear_forward(x, w, b, "silu"), steps, warmup)
+        rec("north_star_bf16_linear_bias_silu_4096", ms, 2.0 * 4096 ** 3, 3 * 4096 * 4096 * 2.0, "mfma",
+            PEAK_BF16)
+    return out
+
+
+def cpu_baseline(budget_s: float = 20.0):
+    """The reference CPU path for the headline workload, timed on the host."""
+    from oracle import cpu_path  # the checker package; this leg only
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([p.get("num_threads", 0) for p in threadpool_info()
+                       if p.get("user_api") == "blas"] or [os.cpu_count() or 1])
+    except Exception:  # noqa: BLE001
+        threads = os.cpu_count() or 1
+    rng = np.random.default_rng(7)
+    m = n = k = 4096
+    # bf16 inputs run as fp32 on the reference CPU path (reference dtype.py:31).
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+    b = (rng.standard_normal(n, dtype=np.float32) * np.float32(0.01))
+    gc.disable()
+    try:
+        t0 = time.perf_counter()
+        cpu_path.linear(x, w, b)  # warm-up
+        first = time.perf_counter() - t0
+        trials = int(max(3, min(20, budget_s / max(first, 1e-3))))
+        times = []
+        for _ in range(trials):
+            t0 = time.perf_counter()
+            cpu_path.linear(x, w, b)
+            times.append(time.perf_counter() - t0)
+    finally:
+        gc.enable()
+    med = statistics.median(times)
+    return {"value": round(2.0 * m * n * k / med / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": "reference CPU path (NumPy fp32 x @ W.T + b, nn/layers.py:129-131) at "
+                      "4096x4096x4096, bf16 inputs as fp32 per dtype.py:31; median of %d trials after 1 "
+                      "warm-up, GC off, %d BLAS threads; %.3f s/trial" % (trials, threads, med),
+            "ms_per_step": round(med * 1e3, 2)}
+
+
+def read_traffic():
+    """HBM bytes per launch of the headline kernel from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default=None, help="run only sweep entries containing this text")
+    args = ap.parse_args(argv)
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build runs on one GPU only (the matmul hot path's kernels at one "
+              "GPU's share); --gpus %d is not supported" % max(args.gpus, world), file=sys.stderr)
+        return 2
+
+    d = Dev()
+    cu = d.cu
+    cu.set_device(0)
+    props = cu.get_device_properties(0)
+    log("device:", props)
+    h = headline(d, args.steps, args.warmup)
+    tflops = h["flops"] / (h["ms"] * 1e-3) / 1e12
+    log("headline: %s  %.4f ms  %.1f TFLOP/s  (%.1f%% of %.2f PF)" % (
+        h["kernel"], h["ms"], tflops, 100 * tflops * 1e12 / PEAK_BF16, PEAK_BF16 / 1e15))
+    sw = {} if args.no_sweep else sweep(d, args.steps, args.warmup, args.only)
+    cpu = None if args.no_cpu else cpu_baseline()
+    line = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(h["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "north-star bf16 linear_forward (GEMM + bias epilogue, fp32 accumulate) "
+                               "M=N=K=4096, x~N(0,1), W~N(0,0.02), b~N(0,0.01)",
+                   "M": h["m"], "N": h["n"], "K": h["k"], "epilogue": "bias",
+                   "kernel": h["kernel"], "parallelism": "single-gpu"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16 / 1e12,
+                     "unit": "TFLOP/s", "frac": round(tflops * 1e12 / PEAK_BF16, 4),
+                     "traffic": read_traffic()},
+        "cpu_baseline": cpu,
+        "sweep": sw,
+        "device": {"name": props.get("name"), "arch": props.get("arch"),
+                   "cus": props.get("multi_processor_count")},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
