@@ -252,6 +252,10 @@ def main(argv=None):
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None, help="run only sweep entries containing this text")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run one fp32 x*1.0 pass over 1 GiB (reads 1 GiB, writes 1 GiB): the "
+                         "known-traffic kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--no-headline", action="store_true")
     args = ap.parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -264,6 +268,16 @@ def main(argv=None):
     cu.set_device(0)
     props = cu.get_device_properties(0)
     log("device:", props)
+    if args.copy_calibration:
+        src = cu.zeros(((1 << 30) // 4,), np.float32, 0)
+        cu.device_synchronize()
+        y = cu.dev_muls(src, 1.0)
+        cu.device_synchronize()
+        del y, src
+    if args.no_headline:
+        sw = sweep(d, args.steps, args.warmup, args.only)
+        print(json.dumps({"sweep": sw}), flush=True)
+        return 0
     h = headline(d, args.steps, args.warmup)
     tflops = h["flops"] / (h["ms"] * 1e-3) / 1e12
     log("headline: %s  %.4f ms  %.1f TFLOP/s  (%.1f%% of %.2f PF)" % (

@@ -45,6 +45,7 @@ const char* tile_name(int cfg) {
     case TILE_64x64: return "gemm tile 64x64";
     case TILE_GENERIC: return "gemm tile generic";
     case TILE_SKINNY: return "gemm skinny";
+    case TILE_NT_BIG: return "gemm nt 256x256 lds-dma";
   }
   return "gemm";
 }
@@ -52,6 +53,7 @@ const char* tile_name(int cfg) {
 void tile_dims(int cfg, bool fp32, int& bm, int& bn) {
   switch (cfg) {
     case TILE_256x256: bm = 256; bn = 256; return;
+    case TILE_NT_BIG: bm = 256; bn = 256; return;
     case TILE_256x128: bm = 256; bn = 128; return;
     case TILE_128x128: bm = 128; bn = 128; return;
     case TILE_256x64: bm = 256; bn = 64; return;
@@ -105,12 +107,13 @@ static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Picks the 16-bit tile config.  Largest tile that still gives every CU at
 // least one tile; narrow-N problems (P.V, N <= 64) use the 256x64 tile.
-static int choose_tile16(int64_t M, int64_t N, int64_t batch, bool vec, bool b_kmajor,
+static int choose_tile16(int64_t M, int64_t N, int64_t K, int64_t batch, bool vec, bool b_kmajor,
                          bool f32_out, int cus) {
   if (!vec) return TILE_GENERIC;
   if (b_kmajor && M <= 16) return TILE_SKINNY;
   if (f32_out) return TILE_128x128;
   auto tiles = [&](int64_t bm, int64_t bn) { return cdiv(M, bm) * cdiv(N, bn) * batch; };
+  if (b_kmajor && K >= 128 && K % 128 == 0 && N > 64 && tiles(256, 256) >= cus) return TILE_NT_BIG;
   if (N <= 64) return tiles(256, 64) >= cus ? TILE_256x64 : TILE_64x64;
   if (tiles(256, 256) >= cus) return TILE_256x256;
   if (tiles(256, 128) >= cus) return TILE_256x128;
@@ -223,7 +226,10 @@ static int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K,
                      (strideA % 8 == 0) && (strideB % 8 == 0) && (K % 8 == 0) &&
                      (b_kmajor || N % 8 == 0);
     plan.fp32 = false;
-    plan.cfg = choose_tile16(M, N, batch, vec, b_kmajor, c_dtype == SF_F32, cus);
+    plan.cfg = choose_tile16(M, N, K, batch, vec, b_kmajor, c_dtype == SF_F32, cus);
+    // The LDS-DMA kernel addresses each operand with 32-bit byte offsets.
+    if (plan.cfg == TILE_NT_BIG && (M * lda * 2 >= (int64_t(1) << 31) || N * ldb * 2 >= (int64_t(1) << 31)))
+      plan.cfg = TILE_256x256;
   }
   tile_dims(plan.cfg, plan.fp32, bm, bn);
   if (cdiv(M, bm) * cdiv(N, bn) > INT32_MAX)

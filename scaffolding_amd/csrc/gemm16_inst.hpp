@@ -3,6 +3,7 @@
 #pragma once
 
 #include "sf_internal.hpp"
+#include "gemm16nt_pp.hpp"
 #include "skinny16.hpp"
 
 namespace sf {
@@ -29,6 +30,12 @@ static int launch16_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hi
     case TILE_GENERIC:
       hipLaunchKernelGGL((gemm16_kernel<TIn, TOut, 64, 64, 2, 2, KM, false>), g, dim3(256), 0, st, p);
       break;
+    case TILE_NT_BIG:
+      if constexpr (KM) {
+        hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut>), g, dim3(512), 0, st, p);
+        break;
+      }
+      return fail(SF_ERR_UNSUPPORTED, "the 256x256 NT kernel needs a K-contiguous B");
     case TILE_SKINNY:
       if constexpr (KM) {
         // grid.x = ceil(N / 32): 2 row blocks per workgroup, K split over 4 waves.

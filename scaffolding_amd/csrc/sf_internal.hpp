@@ -24,7 +24,8 @@ enum TileCfg {
   TILE_256x64 = 3,   // 256 threads, waves 4x1 of 64x64 (narrow N, e.g. P.V)
   TILE_64x64 = 4,    // 256 threads, waves 2x2 of 32x32
   TILE_GENERIC = 5,  // 64x64, element-wise bounds-checked loads (any layout)
-  TILE_SKINNY = 6    // M <= 16 stream kernel
+  TILE_SKINNY = 6,   // M <= 16 stream kernel
+  TILE_NT_BIG = 7    // 256x256 NT, 8-wave ping-pong, direct-to-LDS (gemm16nt_pp.hpp)
 };
 const char* tile_name(int cfg);
 

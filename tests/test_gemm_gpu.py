@@ -125,6 +125,9 @@ def test_batched_nt_alpha():
 TILE_CASES = [
     # (dtype, nt, M, N, K, batch, expected kernel)
     ("bfloat16", True, 4096, 4096, 192, 1, "gemm tile 256x256"),
+    ("bfloat16", True, 4096, 4096, 256, 1, "gemm nt 256x256 lds-dma"),
+    ("float16", True, 4000, 4100, 384, 1, "gemm nt 256x256 lds-dma"),
+    ("bfloat16", True, 1000, 1100, 128, 16, "gemm nt 256x256 lds-dma"),
     ("bfloat16", False, 4096, 4096, 192, 1, "gemm tile 256x256"),
     ("float16", True, 2048, 4096, 136, 1, "gemm tile 256x128"),
     ("bfloat16", False, 2048, 4096, 136, 1, "gemm tile 256x128"),
@@ -178,6 +181,26 @@ def test_tile_configs(case):
         eps = 2 * (k * 2.0 ** -23 + {"float32": 2.0 ** -24, "float16": 2.0 ** -11, "bfloat16": 2.0 ** -8}[dtype])
         assert np.all(np.abs(rs - rs64) <= eps * full_abs.sum(axis=1) + 1e-6), "row checksum %s" % (case,)
         assert np.all(np.abs(cs - cs64) <= eps * full_abs.sum(axis=0) + 1e-6), "col checksum %s" % (case,)
+
+
+@pytest.mark.parametrize("act", [None, "silu", "gelu"])
+def test_big_nt_linear_epilogues(act):
+    """The 256x256 LDS-DMA NT kernel with bias and fused activations on ragged
+    edges (M, N not tile multiples), checked on sampled rows and edge rows."""
+    m, n, k = 2100, 8000, 512
+    rng = np.random.default_rng(31)
+    x = rnd(rng, (m, k), 1.0, "bfloat16")
+    w = rnd(rng, (n, k), 1.0 / np.sqrt(k), "bfloat16")
+    b = rnd(rng, (n,), 0.5, "bfloat16")
+    gx, gw, gb = up(x, "bfloat16"), up(w, "bfloat16"), up(b, "bfloat16")
+    plan = cu().gemm_plan(1, m, n, k, 1, gx.data_ptr, k, 0, gw.data_ptr, k, 0, n, 0, gx.dtype,
+                          epi=1, ptr_bias=gb.data_ptr)
+    assert plan.startswith("gemm nt 256x256 lds-dma"), plan
+    y = down(cu().dev_linear_forward(gx, gw, gb, act))
+    rows = np.unique(np.r_[0, 255, 256, 1023, 1024, 2047, 2048, m - 1, np.arange(3, m, 61)])
+    y64 = ref.linear_f64(x[rows], w, b, act)
+    absprod = np.abs(x[rows].astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+    check_bound(y[rows], y64, gemm_bound(y64, absprod, k, "bfloat16", act), "big nt %s" % act)
 
 
 def test_k_zero_writes_epilogue_of_zero():
