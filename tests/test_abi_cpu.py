@@ -1,0 +1,146 @@
+"""The C ABI on the CPU (no GPU needed): libsfgemm loads, exports every
+function include/sfgemm.h declares, validates arguments before touching the
+device (the reference's error convention: 0 ok, negative code, text), and
+the dispatcher picks the documented kernel for each config shape."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sfgemm.h")
+LIB = os.path.join(ROOT, "scaffolding_amd", "libsfgemm.so")
+
+I64 = ctypes.c_int64
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.fail("libsfgemm.so not built: run python -m scaffolding_amd.build")
+    so = ctypes.CDLL(LIB)
+    so.sf_last_error.restype = ctypes.c_char_p
+    so.sf_status_string.restype = ctypes.c_char_p
+    return so
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sf_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared_functions()
+    assert len(names) >= 39
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_status_strings(lib):
+    assert lib.sf_status_string(0) == b"success"
+    assert lib.sf_status_string(-2) == b"invalid argument"
+    assert lib.sf_status_string(-3) == b"unsupported operation"
+    assert lib.sf_version() == 100
+
+
+def gemm(lib, transA=0, transB=1, M=4, N=4, K=4, batch=1, A=256, lda=4, sA=0, B=512, ldb=4, sB=0,
+         C=768, ldc=4, sC=0, ab=2, c=2, alpha=1.0, bias=None, epi=0):
+    return lib.sf_gemm(transA, transB, I64(M), I64(N), I64(K), I64(batch), ctypes.c_void_p(A), I64(lda),
+                       I64(sA), ctypes.c_void_p(B), I64(ldb), I64(sB), ctypes.c_void_p(C), I64(ldc),
+                       I64(sC), ab, c, ctypes.c_float(alpha), ctypes.c_void_p(bias), epi, None)
+
+
+@pytest.mark.parametrize("kw,code,text", [
+    (dict(A=None), -2, b"null operand pointer"),
+    (dict(C=None), -2, b"null operand pointer"),
+    (dict(M=-1), -2, b"negative size"),
+    (dict(transA=1), -3, b"transA"),
+    (dict(ab=2, c=1), -3, b"output dtype"),
+    (dict(ab=7), -2, b"unknown dtype"),
+    (dict(epi=9), -2, b"unknown epilogue"),
+    (dict(epi=1), -2, b"needs a bias"),
+    (dict(bias=1024), -2, b"has no bias"),
+    (dict(lda=3), -2, b"leading dimension"),
+    (dict(transB=0, ldb=3), -2, b"leading dimension"),
+    (dict(batch=2, sC=3), -2, b"overlaps batch"),
+    (dict(M=1 << 31), -2, b"2^31"),
+])
+def test_gemm_validation_without_device(lib, kw, code, text):
+    assert gemm(lib, **kw) == code
+    assert text in lib.sf_last_error()
+
+
+def test_gemm_empty_is_noop(lib):
+    assert gemm(lib, M=0, A=None, B=None, C=None) == 0
+    assert gemm(lib, N=0, A=None, B=None, C=None) == 0
+    assert gemm(lib, batch=0, A=None, B=None, C=None) == 0
+
+
+def test_rowops_validation(lib):
+    assert lib.sf_softmax_rows(None, None, I64(3), I64(4), 0, 0, ctypes.c_float(1.0), None) == -2
+    assert lib.sf_softmax_rows(None, None, I64(0), I64(4), 0, 0, ctypes.c_float(1.0), None) == 0
+    assert lib.sf_silu(None, None, I64(-1), 0, None) == -2
+    assert lib.sf_cast(None, 0, None, 5, I64(1), None) == -2
+    assert lib.sf_bias_add_rows(None, None, I64(2), I64(2), 0, None) == -2
+
+
+def plan(**kw):
+    from scaffolding_amd import _cuda_ops as cu
+    a = dict(transB=1, M=4096, N=4096, K=4096, batch=1, ptr_a=256, lda=4096, stride_a=0, ptr_b=512,
+             ldb=4096, stride_b=0, ldc=4096, stride_c=0, dtype="bfloat16")
+    a.update(kw)
+    return cu.gemm_plan(a["transB"], a["M"], a["N"], a["K"], a["batch"], a["ptr_a"], a["lda"], a["stride_a"],
+                        a["ptr_b"], a["ldb"], a["stride_b"], a["ldc"], a["stride_c"], a["dtype"])
+
+
+def test_dispatch_for_config_shapes():
+    # north star / C3 M=4096 / C5: large NT -> 8-wave ping-pong kernel
+    assert plan().startswith("gemm nt 256x256 lds-dma")
+    assert plan(M=4096, N=11008, ldc=11008).startswith("gemm nt 256x256 lds-dma")
+    assert plan(M=17776, N=1920, K=7680, lda=7680, ldb=7680, ldc=1920).startswith("gemm nt 256x256 lds-dma")
+    # C3 decode shapes -> stream kernel
+    assert plan(M=1, N=11008, ldc=11008).startswith("gemm skinny")
+    assert plan(M=16, N=11008, ldc=11008).startswith("gemm skinny")
+    # C4: QK^T (K = 64) and P.V (N = 64, B N-contiguous)
+    assert plan(M=4096, N=4096, K=64, batch=60, lda=64, ldb=64, stride_a=4096 * 64, stride_b=4096 * 64,
+                stride_c=4096 * 4096, dtype="float16").startswith("gemm tile 256x256")
+    assert plan(transB=0, M=4096, N=64, K=4096, batch=60, ldb=64, ldc=64, stride_a=4096 * 4096,
+                stride_b=4096 * 64, stride_c=4096 * 64, dtype="float16").startswith("gemm tile 256x64")
+    # C1 / C2 fp32
+    assert plan(M=64, N=512, K=512, lda=512, ldb=512, ldc=512, dtype="float32").startswith("gemm tile 64x64 fp32")
+    assert plan(transB=0, dtype="float32").startswith("gemm tile 128x128 fp32")
+    # unaligned operands fall back to the bounds-checked kernel
+    assert plan(K=4095, lda=4095, ldb=4095).startswith("gemm tile generic")
+    assert plan(ptr_a=258).startswith("gemm tile generic")
+
+
+def test_python_surface_without_device():
+    import numpy as np
+
+    import scaffolding_amd as sf
+    assert sf.dtype.from_any("bfloat16") is sf.bfloat16
+    assert sf.dtype.from_any(np.float16) is sf.float16
+    assert sf.bfloat16.to_numpy() == np.float32  # host view, as reference dtype.py:31
+    assert str(sf.device("cuda:1")) == "cuda:1" and sf.device("cuda") == sf.device("cuda:0")
+    t = sf.tensor(np.ones((2, 3), np.float32))
+    assert t.shape == (2, 3) and t.dtype is sf.float32 and not t.is_cuda
+    with pytest.raises(RuntimeError, match="GPU only"):
+        sf.matmul(t, t)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        sf.nn.functional.linear(t, t)
+    with pytest.raises(TypeError):
+        sf.tensor(np.ones(3), dtype="bfloat16")
+    assert sf.cuda.device_count() >= 0
+
+
+def test_bench_refuses_multi_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
