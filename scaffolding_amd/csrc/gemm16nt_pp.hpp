@@ -24,12 +24,15 @@
 // references are static).  Operand tiles reach LDS through gfx950's
 // direct-to-LDS load (global_load_lds_dwordx4: lane l's 16 bytes land at
 // base + 16 l), so no VGPRs or ds_write instructions carry them.  A slice
-// row is 32 elements = 64 bytes = four 16-byte chunks; chunk c of row r is
-// stored at slot c ^ ((r >> 2) & 3).  Sixteen lanes reading one chunk of
-// rows r0..r0+15 then hit sixteen distinct 16-byte bank groups, so
-// ds_read_b128 is conflict-free; a direct-load instruction fills 16
-// consecutive rows slot by slot, so lane l fetches chunk
-// (l & 3) ^ ((l >> 4) & 3) of row l >> 2.  Rows past M or N are clamped to
+// row is 32 elements = 64 bytes = four 16-byte chunks.  The 16 KB stage is
+// laid out as 128 lines of 128 bytes: line q holds rows q and q + 128, and
+// logical chunk h = 4 * (row >> 7) + c sits at slot h ^ (q & 7).  An MFMA
+// fragment (16 consecutive rows, one chunk) then reads 16 lines at 128-byte
+// stride with the slot rotated by the line, which ds_read_b128 serves
+// without bank conflicts (measured: 64-byte-row layouts conflict whatever
+// the chunk swizzle).  A direct-load instruction fills 8 lines slot by
+// slot, so lane l fetches logical chunk (l & 7) ^ (l >> 3) of line l >> 3.
+// Rows past M or N are clamped to
 // the last valid row (their products only reach unstored outputs);
 // K % 128 == 0 is required.  Slice t is read by
 // group 0 between barriers 2t and 2t+1 and by group 1 between 2t+1 and
@@ -94,11 +97,14 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   const int M = p.M, N = p.N, K = p.K;
   const int KT = K / BK;  // multiple of 4
 
-  // Direct loads: instruction i of this wave fills tile rows wave*32 + 16 i
-  // .. +15; lane l takes row + (l >> 2), chunk (l & 3) ^ ((l >> 4) & 3).
-  const uint32_t dchunk_b = (uint32_t)(((lane & 3) ^ ((lane >> 4) & 3)) * 16);
-  const int ra0 = m0 + wave * 32 + (lane >> 2);
-  const int rb0 = n0 + wave * 32 + (lane >> 2);
+  // Direct loads: instruction i of this wave fills lines wave*16 + 8 i .. +7;
+  // lane l takes line + (l >> 3), logical chunk h = (l & 7) ^ (l >> 3), i.e.
+  // row line + 128 (h >> 2), chunk h & 3.
+  const int dh = (lane & 7) ^ (lane >> 3);
+  const uint32_t dchunk_b = (uint32_t)((dh & 3) * 16);
+  const int drow = wave * 16 + (lane >> 3) + (dh >> 2) * 128;
+  const int ra0 = m0 + drow;
+  const int rb0 = n0 + drow;
   const uint32_t lda_b = (uint32_t)p.lda * 2u, ldb_b = (uint32_t)p.ldb * 2u;
   const char* Ab = reinterpret_cast<const char*>(A);
   const char* Bb = reinterpret_cast<const char*>(B);
@@ -107,11 +113,11 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
     const char* bk = Bb + (size_t)k0 * 2;
 #pragma unroll
     for (int i = 0; i < DMA_I; ++i) {
-      const int ga = ra0 + i * 16, gb = rb0 + i * 16;
+      const int ga = ra0 + i * 8, gb = rb0 + i * 8;
       const uint32_t oa = (uint32_t)(ga < M ? ga : M - 1) * lda_b + dchunk_b;
       const uint32_t ob = (uint32_t)(gb < N ? gb : N - 1) * ldb_b + dchunk_b;
-      dma16(ak + oa, sA + (wave * 32 + i * 16) * 64);
-      dma16(bk + ob, sB + (wave * 32 + i * 16) * 64);
+      dma16(ak + oa, sA + (wave * 16 + i * 8) * 128);
+      dma16(bk + ob, sB + (wave * 16 + i * 8) * 128);
     }
   };
 
@@ -122,9 +128,12 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
     for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   u32x4 ya[FM], xb[FN];
 
-  const int fslot = ((lane >> 4) ^ ((lane >> 2) & 3)) << 4;
-  const int fa = (wm * WM + (lane & 15)) * 64 + fslot;
-  const int fb = (wn * WN + (lane & 15)) * 64 + fslot;
+  // Fragment byte offsets: A block j reads rows wm*128 + 16 j + (l & 15),
+  // i.e. lines 16 j + (l & 15), logical chunk 4 wm + (l >> 4); B block i
+  // reads rows wn*64 + 16 i + (l & 15), i.e. lines 64 (wn & 1) + 16 i +
+  // (l & 15), logical chunk 4 (wn >> 1) + (l >> 4).  Blocks are 2 KB apart.
+  const int fa = (lane & 15) * 128 + (((wm * 4 + (lane >> 4)) ^ (lane & 7)) << 4);
+  const int fb = ((wn & 1) * 64 + (lane & 15)) * 128 + ((((wn >> 1) * 4 + (lane >> 4)) ^ (lane & 7)) << 4);
 
   // Waits: own direct loads of slice t+1 landed; slices after it that this
   // wave already issued (at most two) may still be in flight.
@@ -142,9 +151,9 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
     // memory phase
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int j = 0; j < FM; ++j) ya[j] = *reinterpret_cast<const u32x4*>(sA + fa + j * 1024);
+    for (int j = 0; j < FM; ++j) ya[j] = *reinterpret_cast<const u32x4*>(sA + fa + j * 2048);
 #pragma unroll
-    for (int i = 0; i < FN; ++i) xb[i] = *reinterpret_cast<const u32x4*>(sB + fb + i * 1024);
+    for (int i = 0; i < FN; ++i) xb[i] = *reinterpret_cast<const u32x4*>(sB + fb + i * 2048);
     if (t + 3 < KT) dma(nA, nB, (t + 3) * BK);
     if (grp == 1)
       wait_next(t);
