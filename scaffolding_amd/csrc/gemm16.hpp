@@ -300,22 +300,25 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmParam
   const int act = epi_act(p.epi);
   const float alpha = p.alpha;
   const bool vec_ok = ((p.ldc & 3) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
+  with_act(act, [&](auto act_c) {
+    constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
-  for (int i = 0; i < FN; ++i) {
-    const int n = n0 + wn * WN + i * 16 + 4 * (lane >> 4);
-    float bv[4] = {0.f, 0.f, 0.f, 0.f};
-    if (has_bias) load_bias4<TIn>(p.bias, n, N, bv);
+    for (int i = 0; i < FN; ++i) {
+      const int n = n0 + wn * WN + i * 16 + 4 * (lane >> 4);
+      float bv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (has_bias) load_bias4<TIn>(p.bias, n, N, bv);
 #pragma unroll
-    for (int j = 0; j < FM; ++j) {
-      const int m = m0 + wm * WM + j * 16 + (lane & 15);
-      if (m < M && n < N) {
-        float v[4];
+      for (int j = 0; j < FM; ++j) {
+        const int m = m0 + wm * WM + j * 16 + (lane & 15);
+        if (m < M && n < N) {
+          float v[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = apply_act(act, acc[i][j][q] * alpha + bv[q]);
-        Store4<TOut>::run(C + (int64_t)m * p.ldc, n, N, vec_ok, v);
+          for (int q = 0; q < 4; ++q) v[q] = act_t<ACT>(acc[i][j][q] * alpha + bv[q]);
+          Store4<TOut>::run(C + (int64_t)m * p.ldc, n, N, vec_ok, v);
+        }
       }
     }
-  }
+  });
 }
 
 }  // namespace sf

@@ -60,6 +60,24 @@ __device__ __forceinline__ void dma16(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds((gbl_ptr_t)g, (lds_ptr_t)lds, 16, 0, 0);
 }
 
+// ds_read_b128 of 16 bytes at LDS byte address `addr` + OFF, issued as inline
+// assembly.  The compiler cannot tell which LDS array a direct load writes,
+// so for an ordinary LDS load it waits for every direct load in flight
+// (vmcnt(0)), which would drain the prefetch queue each k-step; this form
+// carries no such wait.  The caller orders it with explicit s_waitcnt:
+// lgkmcnt before the data is used, and the vmcnt + barrier protocol below
+// before the bytes it reads are valid.
+template <int OFF>
+__device__ __forceinline__ u32x4 ds_read16(uint32_t addr) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 // s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] |
 // lgkmcnt[11:8] | vmcnt[5:4] << 14); counts not being waited on are at max.
 constexpr int waitcnt_imm(int vm, int lgkm) {
@@ -150,10 +168,19 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   auto step = [&](int t, const uint8_t* sA, const uint8_t* sB, uint8_t* nA, uint8_t* nB) {
     // memory phase
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int j = 0; j < FM; ++j) ya[j] = *reinterpret_cast<const u32x4*>(sA + fa + j * 2048);
-#pragma unroll
-    for (int i = 0; i < FN; ++i) xb[i] = *reinterpret_cast<const u32x4*>(sB + fb + i * 2048);
+    const uint32_t la = lds_addr(sA) + fa, lb = lds_addr(sB) + fb;
+    ya[0] = ds_read16<0 * 2048>(la);
+    ya[1] = ds_read16<1 * 2048>(la);
+    ya[2] = ds_read16<2 * 2048>(la);
+    ya[3] = ds_read16<3 * 2048>(la);
+    ya[4] = ds_read16<4 * 2048>(la);
+    ya[5] = ds_read16<5 * 2048>(la);
+    ya[6] = ds_read16<6 * 2048>(la);
+    ya[7] = ds_read16<7 * 2048>(la);
+    xb[0] = ds_read16<0 * 2048>(lb);
+    xb[1] = ds_read16<1 * 2048>(lb);
+    xb[2] = ds_read16<2 * 2048>(lb);
+    xb[3] = ds_read16<3 * 2048>(lb);
     if (t + 3 < KT) dma(nA, nB, (t + 3) * BK);
     if (grp == 1)
       wait_next(t);
@@ -214,6 +241,8 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   constexpr int ROWS_I = 64 / LANES_ROW;
   uint16_t* C = static_cast<uint16_t*>(p.C) + b * p.sC;
   const bool vec_ok = ((p.ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
+  with_act(act, [&](auto act_c) {
+  constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
   for (int ps = 0; ps < WM / ROWS_S; ++ps) {
     __syncthreads();
@@ -225,7 +254,7 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
       for (int i = 0; i < FN; ++i) {
         float v[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = apply_act(act, acc[i][j][q] * alpha + bv[i][q]);
+        for (int q = 0; q < 4; ++q) v[q] = act_t<ACT>(acc[i][j][q] * alpha + bv[i][q]);
         const uint32_t lo = Elem<TOut>::from_f32(v[0]) | ((uint32_t)Elem<TOut>::from_f32(v[1]) << 16);
         const uint32_t hi = Elem<TOut>::from_f32(v[2]) | ((uint32_t)Elem<TOut>::from_f32(v[3]) << 16);
         *reinterpret_cast<u32x2*>(stage + r * PITCH + (i * 16 + 4 * (lane >> 4)) * 2) = u32x2{lo, hi};
@@ -251,6 +280,7 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
       }
     }
   }
+  });
 }
 
 }  // namespace sf

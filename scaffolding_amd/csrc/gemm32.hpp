@@ -188,25 +188,28 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm32_kernel(GemmParam
   const float alpha = p.alpha;
   const bool vec_ok = ((p.ldc & 3) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
   const float* bias = static_cast<const float*>(p.bias);
+  with_act(act, [&](auto act_c) {
+    constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
-  for (int i = 0; i < FN; ++i) {
-    const int n = n0 + wn * WN + i * 16 + 4 * g;
-    float bv[4] = {0.f, 0.f, 0.f, 0.f};
-    if (has_bias) {
+    for (int i = 0; i < FN; ++i) {
+      const int n = n0 + wn * WN + i * 16 + 4 * g;
+      float bv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (has_bias) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) bv[q] = (n + q < N) ? bias[n + q] : 0.f;
-    }
+        for (int q = 0; q < 4; ++q) bv[q] = (n + q < N) ? bias[n + q] : 0.f;
+      }
 #pragma unroll
-    for (int j = 0; j < FM; ++j) {
-      const int m = m0 + wm * WM + j * 16 + (lane & 15);
-      if (m < M && n < N) {
-        float v[4];
+      for (int j = 0; j < FM; ++j) {
+        const int m = m0 + wm * WM + j * 16 + (lane & 15);
+        if (m < M && n < N) {
+          float v[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = apply_act(act, acc[i][j][q] * alpha + bv[q]);
-        Store4<float>::run(C + (int64_t)m * p.ldc, n, N, vec_ok, v);
+          for (int q = 0; q < 4; ++q) v[q] = act_t<ACT>(acc[i][j][q] * alpha + bv[q]);
+          Store4<float>::run(C + (int64_t)m * p.ldc, n, N, vec_ok, v);
+        }
       }
     }
-  }
+  });
 }
 
 }  // namespace sf

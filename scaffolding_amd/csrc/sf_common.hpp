@@ -4,6 +4,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 #include <stdint.h>
 
 #include "../../include/sfgemm.h"
@@ -92,10 +94,27 @@ __device__ __forceinline__ float gelu_tanh_f32(float t) {
 // Activation applied after the (optional) bias add.
 enum Act { ACT_NONE = 0, ACT_SILU = 1, ACT_GELU = 2 };
 
-__device__ __forceinline__ float apply_act(int act, float v) {
-  if (act == ACT_SILU) return silu_f32(v);
-  if (act == ACT_GELU) return gelu_tanh_f32(v);
-  return v;
+template <int ACT>
+__device__ __forceinline__ float act_t(float v) {
+  if constexpr (ACT == ACT_SILU)
+    return silu_f32(v);
+  else if constexpr (ACT == ACT_GELU)
+    return gelu_tanh_f32(v);
+  else
+    return v;
+}
+
+// Calls f(std::integral_constant<int, ACT>{}) for the wave-uniform runtime
+// activation `act`: the per-element epilogue is compiled once per activation
+// instead of testing `act` for every value it writes.
+template <typename F>
+__device__ __forceinline__ void with_act(int act, F&& f) {
+  if (act == ACT_SILU)
+    f(std::integral_constant<int, ACT_SILU>{});
+  else if (act == ACT_GELU)
+    f(std::integral_constant<int, ACT_GELU>{});
+  else
+    f(std::integral_constant<int, ACT_NONE>{});
 }
 
 // Decode sf_epilogue into (has_bias, act).

@@ -99,17 +99,20 @@ __global__ __launch_bounds__(KSPLIT * 64) void skinny16_kernel(GemmParams p) {
   const bool vec_ok = ((p.ldc & 3) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
   const int m = lane & 15;
   if (m >= M) return;
+  with_act(act, [&](auto act_c) {
+    constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
-  for (int j = 0; j < NB; ++j) {
-    const int n = n0 + j * 16 + 4 * (lane >> 4);
-    if (n >= N) continue;
-    float bv[4] = {0.f, 0.f, 0.f, 0.f};
-    if (has_bias) load_bias4<TIn>(p.bias, n, N, bv);
-    float v[4];
+    for (int j = 0; j < NB; ++j) {
+      const int n = n0 + j * 16 + 4 * (lane >> 4);
+      if (n >= N) continue;
+      float bv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (has_bias) load_bias4<TIn>(p.bias, n, N, bv);
+      float v[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) v[q] = apply_act(act, acc[j][q] * p.alpha + bv[q]);
-    Store4<TOut>::run(C + (int64_t)m * p.ldc, n, N, vec_ok, v);
-  }
+      for (int q = 0; q < 4; ++q) v[q] = act_t<ACT>(acc[j][q] * p.alpha + bv[q]);
+      Store4<TOut>::run(C + (int64_t)m * p.ldc, n, N, vec_ok, v);
+    }
+  });
 }
 
 }  // namespace sf
