@@ -18,33 +18,30 @@
 // pipe is fed by one wave while its sibling's LDS traffic is in flight.
 // Per wave the loop is  memory(t); barrier; compute(t); barrier.
 //
-// LDS: four stages of the 256 x 32 A and B slices (separate __shared__
-// arrays, so the compiler's wait-count logic can tell a direct load into
-// one stage from ds_reads of another; the loop is unrolled by four so stage
-// references are static).  Operand tiles reach LDS through gfx950's
-// direct-to-LDS load (global_load_lds_dwordx4: lane l's 16 bytes land at
-// base + 16 l), so no VGPRs or ds_write instructions carry them.  A slice
-// row is 32 elements = 64 bytes = four 16-byte chunks.  The 16 KB stage is
-// laid out as 128 lines of 128 bytes: line q holds rows q and q + 128, and
-// logical chunk h = 4 * (row >> 7) + c sits at slot h ^ (q & 7).  An MFMA
-// fragment (16 consecutive rows, one chunk) then reads 16 lines at 128-byte
-// stride with the slot rotated by the line, which ds_read_b128 serves
-// without bank conflicts (measured: 64-byte-row layouts conflict whatever
-// the chunk swizzle).  A direct-load instruction fills 8 lines slot by
-// slot, so lane l fetches logical chunk (l & 7) ^ (l >> 3) of line l >> 3.
-// Rows past M or N are clamped to
-// the last valid row (their products only reach unstored outputs);
-// K % 128 == 0 is required.  Slice t is read by
-// group 0 between barriers 2t and 2t+1 and by group 1 between 2t+1 and
-// 2t+2, so every wave finishes its own loads of slice t before barrier 2t
-// (group 0 at the end of compute(t-1), group 1 at the end of memory(t-1)),
-// and the loads of slice t+3 (issued in memory(t)) only start after the
-// last reads of slice t-1, which sat in the same stage.  Each memory phase
-// ends with its ds_reads complete (lgkmcnt 0) for the same reason.
+// LDS: two stages, each holding a pair of 32-deep k-slices of the 256-row A
+// and B tiles (64 KB per stage, 128 KB in all).  A stage line is one row's
+// 64 k values (128 bytes); its 16-byte chunk h sits at slot h ^ (row & 7),
+// so the 16 rows of an MFMA fragment (one chunk each) fall on 16 distinct
+// bank groups and ds_read_b128 runs without conflicts (measured; layouts of
+// 64-byte rows conflict whatever the swizzle).  Operands move global -> LDS
+// through gfx950's buffer_load_dwordx4 ... lds (lane l's 16 bytes land at
+// the instruction's LDS base + 16 l; no VGPRs or ds_writes), each
+// instruction fetching 8 whole 128-byte rows: full cache lines, twice the
+// useful bytes per request of 64-byte row halves.  Rows past M or N are
+// clamped to the last valid row (their products only reach unstored
+// outputs); K % 128 == 0 is required.
+//
+// Schedule per slice t (group 0 between barriers 2t and 2t+1, group 1 one
+// barrier later): at even t each wave issues its loads of pair t/2 + 1 into
+// the other stage, whose last slice (t-1) both groups finished reading before
+// barrier 2t; before the barrier that precedes slice t+2, every wave waits
+// for its own loads of that pair (vmcnt(0): nothing newer is in flight).
+// Fragment reads are inline-asm ds_read_b128 (see ds_read16), ordered by
+// these explicit waits.
 //
 // Epilogue: alpha, bias and activation in registers, each wave stages its
-// 128 x 64 result through its own LDS array (64-row passes, 144-byte
-// pitch) and stores 128-byte row segments with 16-byte lanes.
+// 128 x 64 result through its own 16 KB of the stage arrays (64-row passes,
+// 144-byte pitch) and stores 128-byte row segments with 16-byte lanes.
 #pragma once
 
 #include "gemm16.hpp"
@@ -52,13 +49,6 @@
 namespace sf {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
-typedef const __attribute__((address_space(1))) void* gbl_ptr_t;
-
-// Direct global -> LDS load of 16 bytes per lane (global_load_lds_dwordx4):
-// lane l's bytes land at LDS address `lds` + 16 l; `lds` is wave-uniform.
-__device__ __forceinline__ void dma16(const void* g, void* lds) {
-  __builtin_amdgcn_global_load_lds((gbl_ptr_t)g, (lds_ptr_t)lds, 16, 0, 0);
-}
 
 // ds_read_b128 of 16 bytes at LDS byte address `addr` + OFF, issued as inline
 // assembly.  The compiler cannot tell which LDS array a direct load writes,
@@ -88,13 +78,10 @@ template <typename TIn, typename TOut>
 __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   constexpr int BM = 256, BN = 256, BK = 32;
   constexpr int WM = 128, WN = 64, FM = WM / 16, FN = WN / 16;
-  constexpr int OP_BYTES = BM * BK * 2;  // 16 KB per operand per stage
-  constexpr int DMA_I = 2;               // per operand per wave per slice (32 rows)
-  constexpr int DPT = 2 * DMA_I;         // direct loads per wave per slice
+  constexpr int OP_BYTES = BM * 2 * BK * 2;  // 32 KB: one operand, two slices
+  constexpr int DMA_I = 4;                   // per operand per wave per slice pair
   __shared__ __attribute__((aligned(1024))) uint8_t sA0[OP_BYTES], sB0[OP_BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t sA1[OP_BYTES], sB1[OP_BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t sA2[OP_BYTES], sB2[OP_BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t sA3[OP_BYTES], sB3[OP_BYTES];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -114,28 +101,37 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   const uint16_t* __restrict__ B = static_cast<const uint16_t*>(p.B) + b * p.sB;
   const int M = p.M, N = p.N, K = p.K;
   const int KT = K / BK;  // multiple of 4
+  const int KP = KT / 2;  // slice pairs
 
-  // Direct loads: instruction i of this wave fills lines wave*16 + 8 i .. +7;
-  // lane l takes line + (l >> 3), logical chunk h = (l & 7) ^ (l >> 3), i.e.
-  // row line + 128 (h >> 2), chunk h & 3.
+  // A pair stage holds 64 k-columns: line r (128 B) is row r's 64 k values,
+  // logical 16-byte chunk h (k = 8h .. 8h+7) at slot h ^ (r & 7).  Slice 2s
+  // of the pair is chunks 0-3, slice 2s+1 chunks 4-7.  Direct loads fetch
+  // whole 128-byte rows: instruction i of this wave fills lines wave*32 +
+  // 8 i .. +7, lane l line + (l >> 3), slot l & 7, i.e. chunk (l&7)^(l>>3).
   const int dh = (lane & 7) ^ (lane >> 3);
-  const uint32_t dchunk_b = (uint32_t)((dh & 3) * 16);
-  const int drow = wave * 16 + (lane >> 3) + (dh >> 2) * 128;
-  const int ra0 = m0 + drow;
-  const int rb0 = n0 + drow;
-  const uint32_t lda_b = (uint32_t)p.lda * 2u, ldb_b = (uint32_t)p.ldb * 2u;
-  const char* Ab = reinterpret_cast<const char*>(A);
-  const char* Bb = reinterpret_cast<const char*>(B);
+  const uint32_t dchunk_b = (uint32_t)(dh * 16);
+  const int drow = wave * 32 + (lane >> 3);
+  // Buffer resources over A's and B's rows of this batch; per-lane 32-bit
+  // row offsets (rows past M / N clamped to the last row: their products
+  // only reach unstored outputs) are fixed for the whole loop, the k offset
+  // goes in the scalar offset.  Every byte read lies below rows * ld * 2.
+  const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)A, (short)0, (int)((uint32_t)M * (uint32_t)p.lda * 2u), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)B, (short)0, (int)((uint32_t)N * (uint32_t)p.ldb * 2u), 0x00020000);
+  uint32_t voa[DMA_I], vob[DMA_I];
+#pragma unroll
+  for (int i = 0; i < DMA_I; ++i) {
+    const int ga = m0 + drow + i * 8, gb = n0 + drow + i * 8;
+    voa[i] = (uint32_t)(ga < M ? ga : M - 1) * (uint32_t)p.lda * 2u + dchunk_b;
+    vob[i] = (uint32_t)(gb < N ? gb : N - 1) * (uint32_t)p.ldb * 2u + dchunk_b;
+  }
   auto dma = [&](uint8_t* sA, uint8_t* sB, int k0) {
-    const char* ak = Ab + (size_t)k0 * 2;
-    const char* bk = Bb + (size_t)k0 * 2;
+    const int so = k0 * 2;
 #pragma unroll
     for (int i = 0; i < DMA_I; ++i) {
-      const int ga = ra0 + i * 8, gb = rb0 + i * 8;
-      const uint32_t oa = (uint32_t)(ga < M ? ga : M - 1) * lda_b + dchunk_b;
-      const uint32_t ob = (uint32_t)(gb < N ? gb : N - 1) * ldb_b + dchunk_b;
-      dma16(ak + oa, sA + (wave * 16 + i * 8) * 128);
-      dma16(bk + ob, sB + (wave * 16 + i * 8) * 128);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_ptr_t)(sA + (wave * 32 + i * 8) * 128), 16, voa[i], so, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_ptr_t)(sB + (wave * 32 + i * 8) * 128), 16, vob[i], so, 0, 0);
     }
   };
 
@@ -146,29 +142,17 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
     for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   u32x4 ya[FM], xb[FN];
 
-  // Fragment byte offsets: A block j reads rows wm*128 + 16 j + (l & 15),
-  // i.e. lines 16 j + (l & 15), logical chunk 4 wm + (l >> 4); B block i
-  // reads rows wn*64 + 16 i + (l & 15), i.e. lines 64 (wn & 1) + 16 i +
-  // (l & 15), logical chunk 4 (wn >> 1) + (l >> 4).  Blocks are 2 KB apart.
-  const int fa = (lane & 15) * 128 + (((wm * 4 + (lane >> 4)) ^ (lane & 7)) << 4);
-  const int fb = ((wn & 1) * 64 + (lane & 15)) * 128 + ((((wn >> 1) * 4 + (lane >> 4)) ^ (lane & 7)) << 4);
-
-  // Waits: own direct loads of slice t+1 landed; slices after it that this
-  // wave already issued (at most two) may still be in flight.
-  auto wait_next = [&](int t) {
-    const int pend = KT - 2 - t;  // slices t+2 .. min(t+3, KT-1) issued
-    if (pend >= 2)
-      __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * DPT, 0));
-    else if (pend == 1)
-      __builtin_amdgcn_s_waitcnt(waitcnt_imm(DPT, 0));
-    else
-      __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
-  };
+  // Fragment byte offsets for slice half 0: A block j reads lines wm*128 +
+  // 16 j + (l & 15), chunk l >> 4; B block i lines wn*64 + 16 i + (l & 15).
+  // Half 1 reads chunk 4 + (l >> 4): its slot differs in bit 2 (byte bit 6).
+  const int fa = (wm * 128 + (lane & 15)) * 128 + (((lane >> 4) ^ (lane & 7)) << 4);
+  const int fb = (wn * 64 + (lane & 15)) * 128 + (((lane >> 4) ^ (lane & 7)) << 4);
 
   auto step = [&](int t, const uint8_t* sA, const uint8_t* sB, uint8_t* nA, uint8_t* nB) {
+    const bool odd = t & 1;  // static after unrolling
     // memory phase
     __builtin_amdgcn_sched_barrier(0);
-    const uint32_t la = lds_addr(sA) + fa, lb = lds_addr(sB) + fb;
+    const uint32_t la = lds_addr(sA) + (odd ? (fa ^ 64) : fa), lb = lds_addr(sB) + (odd ? (fb ^ 64) : fb);
     ya[0] = ds_read16<0 * 2048>(la);
     ya[1] = ds_read16<1 * 2048>(la);
     ya[2] = ds_read16<2 * 2048>(la);
@@ -181,9 +165,13 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
     xb[1] = ds_read16<1 * 2048>(lb);
     xb[2] = ds_read16<2 * 2048>(lb);
     xb[3] = ds_read16<3 * 2048>(lb);
-    if (t + 3 < KT) dma(nA, nB, (t + 3) * BK);
-    if (grp == 1)
-      wait_next(t);
+    // Even t: the other pair stage was last read in step t-1, which both
+    // groups finished before this phase; fill it with pair t/2 + 1.
+    if (!odd && t / 2 + 1 < KP) dma(nA, nB, (t + 2) * BK);
+    // Before step t+1 may read: if t+1 starts a new pair, this wave's loads of
+    // that pair (issued in step t-1, nothing later yet) have landed.
+    if (grp == 1 && odd)
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
     else
       __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
     __builtin_amdgcn_s_barrier();
@@ -194,21 +182,19 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
 #pragma unroll
       for (int j = 0; j < FM; ++j) acc[i][j] = Mfma16<TIn>::run(xb[i], ya[j], acc[i][j]);
     __builtin_amdgcn_sched_barrier(0);
-    if (grp == 0) wait_next(t);
+    if (grp == 0 && odd) __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 63));
     __builtin_amdgcn_s_barrier();
   };
 
   dma(sA0, sB0, 0);
-  dma(sA1, sB1, BK);
-  dma(sA2, sB2, 2 * BK);
-  __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * DPT, 0));  // own part of slice 0
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
   __builtin_amdgcn_s_barrier();
   if (grp == 1) __builtin_amdgcn_s_barrier();
   for (int t = 0; t < KT; t += 4) {
-    step(t + 0, sA0, sB0, sA3, sB3);
-    step(t + 1, sA1, sB1, sA0, sB0);
-    step(t + 2, sA2, sB2, sA1, sB1);
-    step(t + 3, sA3, sB3, sA2, sB2);
+    step(t + 0, sA0, sB0, sA1, sB1);
+    step(t + 1, sA0, sB0, sA1, sB1);
+    step(t + 2, sA1, sB1, sA0, sB0);
+    step(t + 3, sA1, sB1, sA0, sB0);
   }
   if (grp == 0) __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
@@ -225,16 +211,13 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
     if (has_bias) load_bias4<TIn>(p.bias, n0 + wn * WN + i * 16 + 4 * (lane >> 4), N, bv[i]);
   }
   uint8_t* stage;
-  switch (wave) {
+  switch (wave >> 1) {
     case 0: stage = sA0; break;
     case 1: stage = sB0; break;
     case 2: stage = sA1; break;
-    case 3: stage = sB1; break;
-    case 4: stage = sA2; break;
-    case 5: stage = sB2; break;
-    case 6: stage = sA3; break;
-    default: stage = sB3; break;
+    default: stage = sB1; break;
   }
+  stage += (wave & 1) * (OP_BYTES / 2);
   constexpr int PITCH = WN * 2 + 16;  // 144 bytes
   constexpr int ROWS_S = 64;          // 64 x 144 = 9216 B per pass
   constexpr int LANES_ROW = WN * 2 / 16;
