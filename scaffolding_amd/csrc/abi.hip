@@ -46,6 +46,7 @@ const char* tile_name(int cfg) {
     case TILE_GENERIC: return "gemm tile generic";
     case TILE_SKINNY: return "gemm skinny";
     case TILE_NT_BIG: return "gemm nt 256x256 lds-dma";
+    case TILE_SKINNY_LINE: return "gemm skinny line";
   }
   return "gemm";
 }
@@ -58,6 +59,7 @@ void tile_dims(int cfg, bool fp32, int& bm, int& bn) {
     case TILE_128x128: bm = 128; bn = 128; return;
     case TILE_256x64: bm = 256; bn = 64; return;
     case TILE_SKINNY: bm = 16; bn = 32; return;
+    case TILE_SKINNY_LINE: bm = 16; bn = 64; return;
     default: bm = 64; bn = 64; return;
   }
   (void)fp32;
@@ -110,7 +112,8 @@ static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 static int choose_tile16(int64_t M, int64_t N, int64_t K, int64_t batch, bool vec, bool b_kmajor,
                          bool f32_out, int cus) {
   if (!vec) return TILE_GENERIC;
-  if (b_kmajor && M <= 16) return TILE_SKINNY;
+  if (b_kmajor && M <= 16)
+    return (K == 2048 || K == 4096 || K == 8192) ? TILE_SKINNY_LINE : TILE_SKINNY;
   if (f32_out) return TILE_128x128;
   auto tiles = [&](int64_t bm, int64_t bn) { return cdiv(M, bm) * cdiv(N, bn) * batch; };
   if (b_kmajor && K >= 128 && K % 128 == 0 && N > 64 && tiles(256, 256) >= cus) return TILE_NT_BIG;
@@ -231,12 +234,23 @@ static int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K,
     if (plan.cfg == TILE_NT_BIG && (M * lda * 2 >= (int64_t(1) << 31) || N * ldb * 2 >= (int64_t(1) << 31)))
       plan.cfg = TILE_256x256;
   }
+  // The row-segment skinny kernel addresses 64 rows of W with 32-bit offsets.
+  if (plan.cfg == TILE_SKINNY_LINE && ldb * 2 * 64 >= (int64_t(1) << 31)) plan.cfg = TILE_SKINNY;
   tile_dims(plan.cfg, plan.fp32, bm, bn);
   if (cdiv(M, bm) * cdiv(N, bn) > INT32_MAX)
     return fail(SF_ERR_UNSUPPORTED, "sf_gemm: %lld x %lld output needs more than 2^31 tiles",
                 (long long)M, (long long)N);
   p.tiles_m = (int)cdiv(M, bm);
   p.tiles_n = (int)cdiv(N, bn);
+  p.rows_per = 0;
+  if (plan.cfg == TILE_SKINNY_LINE) {
+    // One workgroup per CU where N allows, at most 64 rows of W each.
+    int64_t rp = cdiv(N, cus);
+    rp = rp < 1 ? 1 : (rp > 64 ? 64 : rp);
+    p.rows_per = (int)rp;
+    p.tiles_m = 1;
+    p.tiles_n = (int)cdiv(N, rp);
+  }
   return SF_OK;
 }
 

@@ -49,6 +49,7 @@ struct GemmParams {
   float alpha;
   int epi;  // sf_epilogue
   int tiles_m, tiles_n;
+  int rows_per;  // skinny line kernel: W rows per workgroup
 };
 
 template <typename T> struct Mfma16;

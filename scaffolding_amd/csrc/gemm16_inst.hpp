@@ -8,6 +8,23 @@
 
 namespace sf {
 
+// Row-segment skinny stream: NW = K / 512 waves (K in {2048, 4096, 8192}).
+template <typename TIn, typename TOut>
+static int launch_skinny_line(const GemmParams& p, const dim3& g, hipStream_t st) {
+  switch (p.K) {
+    case 2048:
+      hipLaunchKernelGGL((skinny16l_kernel<TIn, TOut, 4>), g, dim3(256), 0, st, p);
+      return SF_OK;
+    case 4096:
+      hipLaunchKernelGGL((skinny16l_kernel<TIn, TOut, 8>), g, dim3(512), 0, st, p);
+      return SF_OK;
+    case 8192:
+      hipLaunchKernelGGL((skinny16l_kernel<TIn, TOut, 16>), g, dim3(1024), 0, st, p);
+      return SF_OK;
+  }
+  return fail(SF_ERR_INVALID_ARG, "skinny line kernel: K=%d is not 2048, 4096 or 8192", p.K);
+}
+
 template <typename TIn, typename TOut, bool KM>
 static int launch16_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hipStream_t st) {
   const dim3 g(gx, gy);
@@ -43,6 +60,13 @@ static int launch16_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hi
         break;
       }
       return fail(SF_ERR_UNSUPPORTED, "skinny kernel needs a K-contiguous B");
+    case TILE_SKINNY_LINE:
+      if constexpr (KM) {
+        const int rc = launch_skinny_line<TIn, TOut>(p, g, st);
+        if (rc != SF_OK) return rc;
+        break;
+      }
+      return fail(SF_ERR_UNSUPPORTED, "skinny kernel needs a K-contiguous B");
     default:
       return fail(SF_ERR_INVALID_ARG, "unknown tile config %d", cfg);
   }
@@ -63,6 +87,13 @@ static int launch16_f32out(int cfg, const GemmParams& p, unsigned gx, unsigned g
     case TILE_SKINNY:
       if constexpr (KM) {
         hipLaunchKernelGGL((skinny16_kernel<TIn, float, 4, 2, 8>), g, dim3(256), 0, st, p);
+        break;
+      }
+      return fail(SF_ERR_UNSUPPORTED, "skinny kernel needs a K-contiguous B");
+    case TILE_SKINNY_LINE:
+      if constexpr (KM) {
+        const int rc = launch_skinny_line<TIn, float>(p, g, st);
+        if (rc != SF_OK) return rc;
         break;
       }
       return fail(SF_ERR_UNSUPPORTED, "skinny kernel needs a K-contiguous B");

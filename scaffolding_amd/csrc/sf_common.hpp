@@ -104,6 +104,26 @@ __device__ __forceinline__ float act_t(float v) {
     return v;
 }
 
+// static_for<N>(f): f(std::integral_constant<int, 0>{}) ... f(..., N - 1>{})
+// in order, each index a compile-time constant.
+template <int N>
+struct StaticFor {
+  template <typename F>
+  __device__ __forceinline__ static void run(F&& f) {
+    StaticFor<N - 1>::run(f);
+    f(std::integral_constant<int, N - 1>{});
+  }
+};
+template <>
+struct StaticFor<0> {
+  template <typename F>
+  __device__ __forceinline__ static void run(F&&) {}
+};
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  StaticFor<N>::run(f);
+}
+
 // Calls f(std::integral_constant<int, ACT>{}) for the wave-uniform runtime
 // activation `act`: the per-element epilogue is compiled once per activation
 // instead of testing `act` for every value it writes.

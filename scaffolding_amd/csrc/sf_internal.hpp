@@ -25,7 +25,8 @@ enum TileCfg {
   TILE_64x64 = 4,    // 256 threads, waves 2x2 of 32x32
   TILE_GENERIC = 5,  // 64x64, element-wise bounds-checked loads (any layout)
   TILE_SKINNY = 6,   // M <= 16 stream kernel
-  TILE_NT_BIG = 7    // 256x256 NT, 8-wave ping-pong, direct-to-LDS (gemm16nt_pp.hpp)
+  TILE_NT_BIG = 7,   // 256x256 NT, 8-wave ping-pong, direct-to-LDS (gemm16nt_pp.hpp)
+  TILE_SKINNY_LINE = 8  // M <= 16, K in {2048, 4096, 8192}: row-segment stream (skinny16l)
 };
 const char* tile_name(int cfg);
 

@@ -19,6 +19,7 @@
 #pragma once
 
 #include "gemm16.hpp"
+#include "gemm16nt_pp.hpp"
 
 namespace sf {
 
@@ -112,6 +113,151 @@ __global__ __launch_bounds__(KSPLIT * 64) void skinny16_kernel(GemmParams p) {
       for (int q = 0; q < 4; ++q) v[q] = act_t<ACT>(acc[j][q] * p.alpha + bv[q]);
       Store4<TOut>::run(C + (int64_t)m * p.ldc, n, N, vec_ok, v);
     }
+  });
+}
+
+
+// skinny16l_kernel — the M <= 16 stream for K = 512 * NW (NW waves), reading
+// W in whole 128-byte row segments.
+//
+//   * Workgroup g owns W rows [g * rows_per, min(N, (g + 1) * rows_per)),
+//     rows_per <= 64, in up to four 16-row blocks; wave w owns k in
+//     [512 w, 512 w + 512) of every one of those rows.
+//   * A tile is 16 rows x 64 k (16 x 128 bytes).  Its two loads
+//     (buffer_load_dwordx4 ... lds, rows 0-7 and 8-15) each fetch 8 whole
+//     128-byte row segments straight into the wave's private R-tile LDS
+//     ring, line r = row r with 16-byte chunk h at slot h ^ (r & 7); rows
+//     past the workgroup's last row fall outside the buffer resource and
+//     read as zero without touching memory.  R - 1 tiles stay in flight
+//     behind the one being folded.
+//   * Each tile is two conflict-free ds_read_b128 fragments (k halves) and
+//     two v_mfma_f32_16x16x32 with X = W rows, Y = x rows; x's fragments
+//     for the wave's 512 k are loaded once into 64 VGPRs.
+//   * The NW partial 16x16 blocks are summed through LDS by waves 0..nblk-1,
+//     which apply alpha, bias and activation and store their block: lane l
+//     holds C[m = l % 16][n = 4 (l / 16) + 0..3].
+// Every wave waits only for its own loads (vmcnt) and reads only its own
+// ring, so the loop has no barrier.  Requires 16-byte aligned rows.
+template <typename TIn, typename TOut, int NW, int R = 4>
+__global__ __launch_bounds__(NW * 64) void skinny16l_kernel(GemmParams p) {
+  static_assert(R == 4 || R == 8, "the ring depth divides the 8 tiles of a row block");
+  constexpr int TILE = 2048;  // 16 rows x 128 bytes
+  constexpr int MAXB = 4;     // 16-row blocks per workgroup
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[NW][R * TILE];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b = blockIdx.y;
+  const int M = p.M, N = p.N;
+  const int r0 = blockIdx.x * p.rows_per;
+  const int nrows = (N - r0) < p.rows_per ? (N - r0) : p.rows_per;
+  const int nblk = (nrows + 15) >> 4;
+  const uint16_t* __restrict__ X = static_cast<const uint16_t*>(p.A) + b * p.sA;
+  const uint16_t* W = static_cast<const uint16_t*>(p.B) + b * p.sB + (int64_t)r0 * p.ldb;
+  const uint32_t ldb_b = (uint32_t)p.ldb * 2u;
+  const __amdgpu_buffer_rsrc_t rW =
+      __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, (int)((uint32_t)nrows * ldb_b), 0x00020000);
+  const int kw = wave * 512;
+  uint8_t* myring = &ring[wave][0];
+
+  // W is read once: non-temporal loads (cache-policy bit "nt") stream it
+  // past the caches, measured 6.2-6.3 TB/s against 5.5-5.6 without.
+  constexpr int kNonTemporal = 2;
+  // Load lane mapping: load ih of a tile fills tile rows 8 ih + (l >> 3),
+  // slot l & 7, i.e. chunk (l & 7) ^ (l >> 3) of that row.  The 128-byte
+  // line step goes in the scalar offset: an instruction offset would also
+  // move the LDS destination.
+  const uint32_t vrow = (uint32_t)(lane >> 3) * ldb_b + (uint32_t)kw * 2u +
+                        (uint32_t)(((lane & 7) ^ (lane >> 3)) * 16);
+  auto issue = [&](int blk, auto Lc) {
+    constexpr int L = decltype(Lc)::value;
+    uint8_t* dst = myring + (L % R) * TILE;
+    const uint32_t v0 = vrow + (uint32_t)(blk * 16) * ldb_b;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rW, (lds_ptr_t)dst, 16, v0, L * 128, 0, kNonTemporal);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rW, (lds_ptr_t)(dst + 1024), 16, v0 + 8u * ldb_b, L * 128, 0,
+                                             kNonTemporal);
+  };
+  static_for<R - 1>([&](auto Lc) { issue(0, Lc); });
+
+  // x fragments: slice s (k = kw + 32 s ..) lane l: row m = l & 15, 8 k at
+  // kw + 32 s + 8 (l >> 4); rows past M are zero.
+  u32x4 xf[16];
+  {
+    const int m = lane & 15;
+    const uint16_t* xr = X + (int64_t)(m < M ? m : 0) * p.lda + kw + 8 * (lane >> 4);
+#pragma unroll
+    for (int s = 0; s < 16; ++s)
+      xf[s] = m < M ? *reinterpret_cast<const u32x4*>(xr + 32 * s) : u32x4{0u, 0u, 0u, 0u};
+  }
+
+  // Fragment offsets inside a tile: row l & 15, chunk 4 h + (l >> 4).
+  const int f0 = (lane & 15) * 128 + (((lane >> 4) ^ (lane & 7)) << 4);
+  const uint32_t ring_a = lds_addr(myring);
+
+  f32x4 acc[MAXB];
+#pragma unroll
+  for (int j = 0; j < MAXB; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int T = nblk * 8;  // tiles of this wave
+#pragma unroll
+  for (int blk = 0; blk < MAXB; ++blk) {
+    if (blk < nblk) {
+      static_for<8>([&](auto Lc) {
+        constexpr int L = decltype(Lc)::value;
+        constexpr int LN = (L + R - 1) & 7;
+        const int nb = blk + ((L + R - 1) >> 3);
+        // The fences keep load issue, waits, LDS reads and MFMAs in program
+        // order: the wait counts below count exactly the loads issued above
+        // (plus the older x loads, which complete first).
+        __builtin_amdgcn_sched_barrier(0);
+        if (nb < nblk) issue(nb, std::integral_constant<int, LN>{});
+        __builtin_amdgcn_sched_barrier(0);
+        // Tiles issued after this one: min(R - 1, T - 1 - t), two loads each.
+        const int after = T - 1 - (blk * 8 + L);
+        static_for<R>([&](auto Ac) {
+          constexpr int AF = decltype(Ac)::value;
+          if (AF == R - 1 ? after >= AF : after == AF) __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * AF, 63));
+        });
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t a = ring_a + (L % R) * TILE + f0;
+        const u32x4 w0 = ds_read16<0>(a);       // chunk l >> 4
+        const u32x4 w1 = ds_read16<0>(a ^ 64);  // chunk 4 + (l >> 4): slot bit 2 flipped
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+        __builtin_amdgcn_sched_barrier(0);
+        acc[blk] = Mfma16<TIn>::run(w0, xf[2 * L], acc[blk]);
+        acc[blk] = Mfma16<TIn>::run(w1, xf[2 * L + 1], acc[blk]);
+      });
+    }
+  }
+
+  // Cross-wave reduction: each wave parks its blocks in its own ring.
+  f32x4* park = reinterpret_cast<f32x4*>(myring);
+#pragma unroll
+  for (int j = 0; j < MAXB; ++j)
+    if (j < nblk) park[j * 64 + lane] = acc[j];
+  __syncthreads();
+  if (wave >= nblk) return;
+  const int blk = wave;
+  f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int w = 0; w < NW; ++w) sum += reinterpret_cast<const f32x4*>(&ring[w][0])[blk * 64 + lane];
+
+  typedef typename Elem<TOut>::storage OutS;
+  OutS* C = static_cast<OutS*>(p.C) + b * p.sC;
+  const int m = lane & 15;
+  const int n = r0 + blk * 16 + 4 * (lane >> 4);
+  const int n_end = r0 + nrows;
+  if (m >= M || n >= n_end) return;
+  const bool has_bias = epi_has_bias(p.epi);
+  const bool vec_ok = ((p.ldc & 3) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
+  float bv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (has_bias) load_bias4<TIn>(p.bias, n, n_end, bv);
+  with_act(epi_act(p.epi), [&](auto act_c) {
+    constexpr int ACT = decltype(act_c)::value;
+    float v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = act_t<ACT>(sum[q] * p.alpha + bv[q]);
+    Store4<TOut>::run(C + (int64_t)m * p.ldc, n, n_end, vec_ok, v);
   });
 }
 

@@ -104,9 +104,11 @@ def test_dispatch_for_config_shapes():
     assert plan().startswith("gemm nt 256x256 lds-dma")
     assert plan(M=4096, N=11008, ldc=11008).startswith("gemm nt 256x256 lds-dma")
     assert plan(M=17776, N=1920, K=7680, lda=7680, ldb=7680, ldc=1920).startswith("gemm nt 256x256 lds-dma")
-    # C3 decode shapes -> stream kernel
-    assert plan(M=1, N=11008, ldc=11008).startswith("gemm skinny")
-    assert plan(M=16, N=11008, ldc=11008).startswith("gemm skinny")
+    # C3 decode shapes -> row-segment stream kernel (K = 512 x waves)
+    assert plan(M=1, N=11008, ldc=11008).startswith("gemm skinny line")
+    assert plan(M=16, N=11008, ldc=11008).startswith("gemm skinny line")
+    # other K: the chunked stream kernel
+    assert plan(M=16, N=1920, K=1920, lda=1920, ldb=1920, ldc=1920) == "gemm skinny 16-bit"
     # C4: QK^T (K = 64) and P.V (N = 64, B N-contiguous)
     assert plan(M=4096, N=4096, K=64, batch=60, lda=64, ldb=64, stride_a=4096 * 64, stride_b=4096 * 64,
                 stride_c=4096 * 4096, dtype="float16").startswith("gemm tile 256x256")

@@ -4,6 +4,9 @@ against the reference's CPU fp32 path), through the Cython seam and the C
 ABI."""
 from __future__ import annotations
 
+import ctypes
+import os
+
 import numpy as np
 import pytest
 
@@ -138,7 +141,13 @@ TILE_CASES = [
     ("bfloat16", True, 300, 500, 256, 1, "gemm tile 64x64"),
     ("float16", True, 300, 500, 250, 1, "gemm tile generic"),
     ("bfloat16", False, 300, 500, 250, 1, "gemm tile generic"),
-    ("bfloat16", True, 16, 11008, 4096, 1, "gemm skinny"),
+    ("bfloat16", True, 16, 11008, 4096, 1, "gemm skinny line"),
+    ("bfloat16", True, 1, 11008, 4096, 1, "gemm skinny line"),
+    ("float16", True, 3, 1000, 2048, 1, "gemm skinny line"),
+    ("bfloat16", True, 7, 20001, 8192, 1, "gemm skinny line"),
+    ("float16", True, 16, 37, 4096, 5, "gemm skinny line"),
+    ("bfloat16", True, 2, 16389, 2048, 2, "gemm skinny line"),
+    ("bfloat16", True, 16, 4000, 1920, 1, "gemm skinny"),
     ("float16", True, 5, 333, 1000, 3, "gemm skinny"),
     ("float32", True, 2048, 2048, 136, 1, "gemm tile 128x128"),
     ("float32", False, 2048, 2048, 136, 1, "gemm tile 128x128"),
@@ -201,6 +210,52 @@ def test_big_nt_linear_epilogues(act):
     y64 = ref.linear_f64(x[rows], w, b, act)
     absprod = np.abs(x[rows].astype(np.float64)) @ np.abs(w.astype(np.float64)).T
     check_bound(y[rows], y64, gemm_bound(y64, absprod, k, "bfloat16", act), "big nt %s" % act)
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("act", [None, "silu", "gelu"])
+@pytest.mark.parametrize("mnk", [(1, 11008, 4096), (16, 4099, 2048), (9, 700, 8192)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_skinny_line_linear_epilogues(dtype, act, mnk):
+    """The row-segment skinny stream (K = 512 x waves) with bias and fused
+    activations: every output checked, N not a multiple of 16 or of the
+    rows per workgroup."""
+    m, n, k = mnk
+    rng = np.random.default_rng(m * 7 + n + k)
+    x = rnd(rng, (m, k), 1.0, dtype)
+    w = rnd(rng, (n, k), 1.0 / np.sqrt(k), dtype)
+    b = rnd(rng, (n,), 0.5, dtype)
+    gx, gw, gb = up(x, dtype), up(w, dtype), up(b, dtype)
+    plan = cu().gemm_plan(1, m, n, k, 1, gx.data_ptr, k, 0, gw.data_ptr, k, 0, n, 0, gx.dtype,
+                          epi=1, ptr_bias=gb.data_ptr)
+    assert plan.startswith("gemm skinny line"), plan
+    y = down(cu().dev_linear_forward(gx, gw, gb, act))
+    y64 = ref.linear_f64(x, w, b, act)
+    absprod = np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+    check_bound(y, y64, gemm_bound(y64, absprod, k, dtype, act), "skinny line %s %s %s" % (dtype, act, mnk))
+
+
+def test_skinny_line_fp32_output():
+    """16-bit inputs with an fp32 result through the row-segment stream."""
+    m, n, k = 4, 3000, 4096
+    rng = np.random.default_rng(5)
+    a = rnd(rng, (m, k), 1.0, "bfloat16")
+    w = rnd(rng, (n, k), 1.0 / np.sqrt(k), "bfloat16")
+    ga, gw = up(a, "bfloat16"), up(w, "bfloat16")
+    out = cu().empty((m, n), np.float32, 0)
+    plan = cu().gemm_plan(1, m, n, k, 1, ga.data_ptr, k, 0, gw.data_ptr, k, 0, n, 0, ga.dtype)
+    assert plan.startswith("gemm skinny line"), plan
+    so = ctypes.CDLL(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                                  "scaffolding_amd", "libsfgemm.so"))
+    I64, P = ctypes.c_int64, ctypes.c_void_p
+    rc = so.sf_gemm(0, 1, I64(m), I64(n), I64(k), I64(1), P(ga.data_ptr), I64(k), I64(0), P(gw.data_ptr),
+                    I64(k), I64(0), P(out.data_ptr), I64(n), I64(0), 2, 0, ctypes.c_float(1.0), None, 0, None)
+    assert rc == 0
+    cu().device_synchronize()
+    y = down(out)
+    y64 = a.astype(np.float64) @ w.astype(np.float64).T
+    absprod = np.abs(a.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+    check_bound(y, y64, gemm_bound(y64, absprod, k, "float32"), "skinny line fp32 out")
 
 
 def test_k_zero_writes_epilogue_of_zero():
