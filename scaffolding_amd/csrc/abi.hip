@@ -116,7 +116,8 @@ static int choose_tile16(int64_t M, int64_t N, int64_t K, int64_t batch, bool ve
     return (K == 2048 || K == 4096 || K == 8192) ? TILE_SKINNY_LINE : TILE_SKINNY;
   if (f32_out) return TILE_128x128;
   auto tiles = [&](int64_t bm, int64_t bn) { return cdiv(M, bm) * cdiv(N, bn) * batch; };
-  if (b_kmajor && K >= 128 && K % 128 == 0 && N > 64 && tiles(256, 256) >= cus) return TILE_NT_BIG;
+  if (b_kmajor && (K == 64 || (K >= 128 && K % 128 == 0)) && N > 64 && tiles(256, 256) >= cus)
+    return TILE_NT_BIG;
   if (N <= 64) return tiles(256, 64) >= cus ? TILE_256x64 : TILE_64x64;
   if (tiles(256, 256) >= cus) return TILE_256x256;
   if (tiles(256, 128) >= cus) return TILE_256x128;

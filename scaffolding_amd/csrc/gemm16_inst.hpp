@@ -49,7 +49,10 @@ static int launch16_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hi
       break;
     case TILE_NT_BIG:
       if constexpr (KM) {
-        hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut>), g, dim3(512), 0, st, p);
+        if (p.K == 64)
+          hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut, 1>), g, dim3(512), 0, st, p);
+        else
+          hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut, 2>), g, dim3(512), 0, st, p);
         break;
       }
       return fail(SF_ERR_UNSUPPORTED, "the 256x256 NT kernel needs a K-contiguous B");

@@ -74,8 +74,13 @@ constexpr int waitcnt_imm(int vm, int lgkm) {
   return (vm & 15) | (7 << 4) | ((lgkm & 15) << 8) | (((vm >> 4) & 3) << 14);
 }
 
-template <typename TIn, typename TOut>
+// NSTAGE = 2: the pipelined kernel above, K % 128 == 0.  NSTAGE = 1: K == 64
+// exactly (one slice pair, e.g. attention scores Q.K^T at head size 64): a
+// single 64 KB stage, so two workgroups share a CU and one's stores overlap
+// the other's loads.
+template <typename TIn, typename TOut, int NSTAGE = 2>
 __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
+  static_assert(NSTAGE == 1 || NSTAGE == 2, "one or two pair stages");
   constexpr int BM = 256, BN = 256, BK = 32;
   constexpr int WM = 128, WN = 64, FM = WM / 16, FN = WN / 16;
   constexpr int OP_BYTES = BM * 2 * BK * 2;  // 32 KB: one operand, two slices
@@ -190,11 +195,16 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
   __builtin_amdgcn_s_barrier();
   if (grp == 1) __builtin_amdgcn_s_barrier();
-  for (int t = 0; t < KT; t += 4) {
-    step(t + 0, sA0, sB0, sA1, sB1);
-    step(t + 1, sA0, sB0, sA1, sB1);
-    step(t + 2, sA1, sB1, sA0, sB0);
-    step(t + 3, sA1, sB1, sA0, sB0);
+  if constexpr (NSTAGE == 2) {
+    for (int t = 0; t < KT; t += 4) {
+      step(t + 0, sA0, sB0, sA1, sB1);
+      step(t + 1, sA0, sB0, sA1, sB1);
+      step(t + 2, sA1, sB1, sA0, sB0);
+      step(t + 3, sA1, sB1, sA0, sB0);
+    }
+  } else {
+    step(0, sA0, sB0, sA0, sB0);  // KP == 1: no further pair is loaded
+    step(1, sA0, sB0, sA0, sB0);
   }
   if (grp == 0) __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
@@ -210,16 +220,20 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
     for (int q = 0; q < 4; ++q) bv[i][q] = 0.f;
     if (has_bias) load_bias4<TIn>(p.bias, n0 + wn * WN + i * 16 + 4 * (lane >> 4), N, bv[i]);
   }
+  constexpr int PITCH = WN * 2 + 16;             // 144 bytes
+  constexpr int ROWS_S = NSTAGE == 2 ? 64 : 32;  // 9216 / 4608 B per pass and wave
   uint8_t* stage;
-  switch (wave >> 1) {
-    case 0: stage = sA0; break;
-    case 1: stage = sB0; break;
-    case 2: stage = sA1; break;
-    default: stage = sB1; break;
+  if constexpr (NSTAGE == 2) {
+    switch (wave >> 1) {
+      case 0: stage = sA0; break;
+      case 1: stage = sB0; break;
+      case 2: stage = sA1; break;
+      default: stage = sB1; break;
+    }
+    stage += (wave & 1) * (OP_BYTES / 2);
+  } else {
+    stage = ((wave >> 2) ? sB0 : sA0) + (wave & 3) * (ROWS_S * PITCH);
   }
-  stage += (wave & 1) * (OP_BYTES / 2);
-  constexpr int PITCH = WN * 2 + 16;  // 144 bytes
-  constexpr int ROWS_S = 64;          // 64 x 144 = 9216 B per pass
   constexpr int LANES_ROW = WN * 2 / 16;
   constexpr int ROWS_I = 64 / LANES_ROW;
   uint16_t* C = static_cast<uint16_t*>(p.C) + b * p.sC;

@@ -131,6 +131,8 @@ TILE_CASES = [
     ("bfloat16", True, 4096, 4096, 256, 1, "gemm nt 256x256 lds-dma"),
     ("float16", True, 4000, 4100, 384, 1, "gemm nt 256x256 lds-dma"),
     ("bfloat16", True, 1000, 1100, 128, 16, "gemm nt 256x256 lds-dma"),
+    ("float16", True, 2000, 2100, 64, 8, "gemm nt 256x256 lds-dma"),
+    ("bfloat16", True, 4096, 4096, 64, 1, "gemm nt 256x256 lds-dma"),
     ("bfloat16", False, 4096, 4096, 192, 1, "gemm tile 256x256"),
     ("float16", True, 2048, 4096, 136, 1, "gemm tile 256x128"),
     ("bfloat16", False, 2048, 4096, 136, 1, "gemm tile 256x128"),
