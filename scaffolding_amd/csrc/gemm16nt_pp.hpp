@@ -268,7 +268,7 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
       if (gm < M) {
         uint16_t* crow = C + (int64_t)gm * p.ldc;
         if (vec_ok && gn + 8 <= N) {
-          *reinterpret_cast<u32x4*>(crow + gn) = val;
+          __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(crow + gn));
         } else {
 #pragma unroll
           for (int e = 0; e < 8; ++e)
