@@ -168,9 +168,13 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmParam
       int row = idx / CH, ch = idx % CH;
       int gm = m0 + row, gk = k0 + ch * 8;
       if constexpr (VEC) {
-        ra[i] = (gm < M && gk < K)
-                    ? *reinterpret_cast<const u32x4*>(A + (int64_t)gm * lda + gk)
-                    : u32x4{0u, 0u, 0u, 0u};
+        const u32x4* pa = reinterpret_cast<const u32x4*>(A + (int64_t)gm * lda + gk);
+        // The 256 x 64 tile serves N <= 64 (one tile column): every A row
+        // panel is read exactly once, so it streams past the caches.
+        if constexpr (BM == 256 && BN == 64)
+          ra[i] = (gm < M && gk < K) ? __builtin_nontemporal_load(pa) : u32x4{0u, 0u, 0u, 0u};
+        else
+          ra[i] = (gm < M && gk < K) ? *pa : u32x4{0u, 0u, 0u, 0u};
       } else {
         uint16_t e[8];
 #pragma unroll

@@ -8,17 +8,31 @@ namespace sf {
 // Generic 8-element chunk load/store for any element type.  `vec` selects
 // the 16-byte (16-bit types) / 2x16-byte (fp32) path, else per element.
 template <typename T> struct Chunk8;
+// NT: non-temporal (streaming) access, for tensors larger than the caches.
+template <bool NT, typename V>
+__device__ __forceinline__ V ld16(const V* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+template <bool NT, typename V>
+__device__ __forceinline__ void st16(V* p, V v) {
+  if constexpr (NT) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
 template <> struct Chunk8<float> {
+  template <bool NT = false>
   __device__ __forceinline__ static void load(const void* base, int64_t i, float v[8]) {
     const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + i);
-    f32x4 a = p[0], b = p[1];
+    f32x4 a = ld16<NT>(p), b = ld16<NT>(p + 1);
 #pragma unroll
     for (int e = 0; e < 4; ++e) { v[e] = a[e]; v[e + 4] = b[e]; }
   }
+  template <bool NT = false>
   __device__ __forceinline__ static void store(void* base, int64_t i, const float v[8]) {
     f32x4* p = reinterpret_cast<f32x4*>(static_cast<float*>(base) + i);
-    p[0] = f32x4{v[0], v[1], v[2], v[3]};
-    p[1] = f32x4{v[4], v[5], v[6], v[7]};
+    st16<NT>(p, f32x4{v[0], v[1], v[2], v[3]});
+    st16<NT>(p + 1, f32x4{v[4], v[5], v[6], v[7]});
   }
   __device__ __forceinline__ static float get(const void* base, int64_t i) {
     return static_cast<const float*>(base)[i];
@@ -28,19 +42,21 @@ template <> struct Chunk8<float> {
   }
 };
 template <typename T> struct Chunk8 {  // BF16 / F16
+  template <bool NT = false>
   __device__ __forceinline__ static void load(const void* base, int64_t i, float v[8]) {
-    u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + i);
+    u32x4 w = ld16<NT>(reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + i));
 #pragma unroll
     for (int e = 0; e < 8; ++e)
       v[e] = Elem<T>::to_f32(static_cast<uint16_t>(w[e >> 1] >> ((e & 1) * 16)));
   }
+  template <bool NT = false>
   __device__ __forceinline__ static void store(void* base, int64_t i, const float v[8]) {
     u32x4 w;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
       w[e] = static_cast<uint32_t>(Elem<T>::from_f32(v[2 * e])) |
              (static_cast<uint32_t>(Elem<T>::from_f32(v[2 * e + 1])) << 16);
-    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + i) = w;
+    st16<NT>(reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + i), w);
   }
   __device__ __forceinline__ static float get(const void* base, int64_t i) {
     return Elem<T>::to_f32(static_cast<const uint16_t*>(base)[i]);
@@ -55,7 +71,7 @@ template <typename T> struct Chunk8 {  // BF16 / F16
 // elements per lane; cols <= 512 * CPL, cols % 8 == 0, rows 16-B aligned).
 // One HBM read and one write per element.
 // ---------------------------------------------------------------------
-template <typename TI, typename TO, int CPL>
+template <typename TI, typename TO, int CPL, bool NT>
 __global__ __launch_bounds__(256) void softmax_wave_kernel(const void* __restrict__ x,
                                                            void* __restrict__ y, int64_t rows,
                                                            int cols, float scale) {
@@ -70,7 +86,7 @@ __global__ __launch_bounds__(256) void softmax_wave_kernel(const void* __restric
   for (int c = 0; c < CPL; ++c) {
     const int ch = c * 64 + lane;
     if (ch < nch) {
-      Chunk8<TI>::load(x, base + ch * 8, v[c]);
+      Chunk8<TI>::template load<NT>(x, base + ch * 8, v[c]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         v[c][e] *= scale;
@@ -99,7 +115,7 @@ __global__ __launch_bounds__(256) void softmax_wave_kernel(const void* __restric
     if (ch < nch) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[c][e] *= inv;
-      Chunk8<TO>::store(y, base + ch * 8, v[c]);
+      Chunk8<TO>::template store<NT>(y, base + ch * 8, v[c]);
     }
   }
 }
@@ -224,16 +240,26 @@ static void softmax_launch_t(const void* x, void* y, int64_t rows, int64_t cols,
   if (vec) {
     const unsigned grid = static_cast<unsigned>((rows + 3) / 4);
     const int c = static_cast<int>(cols);
+    // Past the 256 MB Infinity Cache nothing stays cached for the consumer:
+    // stream input and output non-temporally.
+    const bool nt = (double)rows * (double)cols * (double)sizeof(typename Elem<TI>::storage) > 256.0 * (1 << 20);
+    auto go = [&](auto cpl_c) {
+      constexpr int CPL = decltype(cpl_c)::value;
+      if (nt)
+        hipLaunchKernelGGL((softmax_wave_kernel<TI, TO, CPL, true>), dim3(grid), dim3(256), 0, st, x, y, rows, c, scale);
+      else
+        hipLaunchKernelGGL((softmax_wave_kernel<TI, TO, CPL, false>), dim3(grid), dim3(256), 0, st, x, y, rows, c, scale);
+    };
     if (cols <= 512)
-      hipLaunchKernelGGL((softmax_wave_kernel<TI, TO, 1>), dim3(grid), dim3(256), 0, st, x, y, rows, c, scale);
+      go(std::integral_constant<int, 1>{});
     else if (cols <= 1024)
-      hipLaunchKernelGGL((softmax_wave_kernel<TI, TO, 2>), dim3(grid), dim3(256), 0, st, x, y, rows, c, scale);
+      go(std::integral_constant<int, 2>{});
     else if (cols <= 2048)
-      hipLaunchKernelGGL((softmax_wave_kernel<TI, TO, 4>), dim3(grid), dim3(256), 0, st, x, y, rows, c, scale);
+      go(std::integral_constant<int, 4>{});
     else if (cols <= 4096)
-      hipLaunchKernelGGL((softmax_wave_kernel<TI, TO, 8>), dim3(grid), dim3(256), 0, st, x, y, rows, c, scale);
+      go(std::integral_constant<int, 8>{});
     else
-      hipLaunchKernelGGL((softmax_wave_kernel<TI, TO, 16>), dim3(grid), dim3(256), 0, st, x, y, rows, c, scale);
+      go(std::integral_constant<int, 16>{});
   } else {
     hipLaunchKernelGGL((softmax_block_kernel<TI, TO>), dim3(static_cast<unsigned>(rows)), dim3(256), 0,
                        st, x, y, rows, cols, scale);
