@@ -164,9 +164,12 @@ def sweep(d: Dev, steps: int, warmup: int, only: str | None):
         ms = d.time_steps(lambda i: cu.dev_batched_matmul(probs, v), st, 2)
         rec("C4_fp16_pv", ms, 2.0 * bh * s * s * dd, bh * (s * s + 2 * s * dd) * 2.0, "hbm", PEAK_BF16)
         del probs
-        ms = d.time_steps(lambda i: cu.dev_scaled_dot_product_attention(q, kk, v, 0.125), st, 1)
+        ms = d.time_steps(lambda i: cu.dev_sdpa_unfused(q, kk, v, 0.125), st, 1)
         rec("C4_fp16_sdpa_3kernel", ms, 4.0 * bh * s * s * dd, bh * (4 * s * dd + 4 * s * s) * 2.0, "hbm",
             PEAK_BF16)
+        # One fused launch (sf_attention): compute-bound, 4 * S^2 * D flop per head.
+        ms = d.time_steps(lambda i: cu.dev_scaled_dot_product_attention(q, kk, v, 0.125), max(5, steps // 2), 2)
+        rec("C4_fp16_sdpa_fused", ms, 4.0 * bh * s * s * dd, bh * 4 * s * dd * 2.0, "mfma", PEAK_BF16)
 
     # C5: bf16 DiT projections, 17776 tokens.
     tokens = 13 * (60 * 90 // 4) + 226

@@ -125,6 +125,24 @@ int sf_gemm_plan(int transA, int transB,
                  sf_dtype ab_dtype, sf_dtype c_dtype, float alpha,
                  const void* bias, sf_epilogue epi, char* buf, int len);
 
+/* Fused attention forward, head size D = 64:
+ *   O[b] = softmax(scale * Q[b] K[b]^T) V[b],   b in [0, batch),
+ * Q[b] Sq x 64, K[b] and V[b] Sk x 64, O[b] Sq x 64, row strides ld*,
+ * batch strides stride* (elements), 16-bit dtype (F16 or BF16), fp32
+ * accumulation and softmax.  One launch; the Sq x Sk scores never reach
+ * memory.  Replaces the three-launch GPU path of
+ * scaled_dot_product_attention (nn/functional.py:310-321: dev_batched_matmul_nt,
+ * dev_muls, dev_softmax, dev_batched_matmul) when there is no mask and no
+ * dropout.  Requires D == 64, Sk % 64 == 0, 16-byte aligned rows
+ * (SF_ERR_UNSUPPORTED otherwise: callers fall back to sf_gemm +
+ * sf_softmax_rows). */
+int sf_attention(const void* Q, int64_t ldq, int64_t strideQ,
+                 const void* K, int64_t ldk, int64_t strideK,
+                 const void* V, int64_t ldv, int64_t strideV,
+                 void* O, int64_t ldo, int64_t strideO,
+                 int64_t batch, int64_t Sq, int64_t Sk, int64_t D,
+                 float scale, sf_dtype dtype, void* stream);
+
 /* Row softmax: y[r,:] = softmax(scale * x[r,:]) for r in [0, rows).
  * Contiguous rows of `cols` elements.  Replaces cuda_softmax_f32
  * (_cuda_kernels.cu:473-640, decl _cuda_ops_decl.h:78-79) with the

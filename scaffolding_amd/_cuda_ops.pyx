@@ -66,6 +66,12 @@ cdef extern from "sfgemm.h" nogil:
                      void* C, int64_t ldc, int64_t strideC,
                      sf_dtype ab_dtype, sf_dtype c_dtype, float alpha,
                      const void* bias, sf_epilogue epi, char* buf, int len)
+    int sf_attention(const void* Q, int64_t ldq, int64_t strideQ,
+                     const void* K, int64_t ldk, int64_t strideK,
+                     const void* V, int64_t ldv, int64_t strideV,
+                     void* O, int64_t ldo, int64_t strideO,
+                     int64_t batch, int64_t Sq, int64_t Sk, int64_t D,
+                     float scale, sf_dtype dtype, void* stream)
     int sf_softmax_rows(const void* x, void* y, int64_t rows, int64_t cols,
                         sf_dtype in_dtype, sf_dtype out_dtype, float scale, void* stream)
     int sf_silu(const void* x, void* y, int64_t n, sf_dtype dt, void* stream)
@@ -740,16 +746,53 @@ def dev_softmax(gt, int dim=-1, float scale=1.0):
     return out
 
 
-def dev_scaled_dot_product_attention(q, k, v, scale=None):
-    """softmax(scale * Q K^T) V with the scale folded into the QK^T epilogue:
-    three launches (QK^T, row softmax, PV), scores kept in the input dtype.
-    q, k, v: (..., S, D)  (reference GPU path nn/functional.py:310-321)."""
+def dev_sdpa_unfused(q, k, v, scale=None):
+    """softmax(scale * Q K^T) V in three launches (QK^T with the scale folded
+    into its epilogue, row softmax, PV), scores kept in the input dtype:
+    the reference GPU path's structure (nn/functional.py:310-321)."""
     d = q.shape[-1]
     s = (1.0 / float(d) ** 0.5) if scale is None else float(scale)
     scores = dev_batched_matmul_nt(q, k, s)
     probs = dev_softmax(scores, -1)
     del scores
     return dev_batched_matmul(probs, v)
+
+
+def dev_scaled_dot_product_attention(q, k, v, scale=None):
+    """softmax(scale * Q K^T) V  (reference GPU path nn/functional.py:310-321).
+    q (..., Sq, D), k and v (..., Sk, D) with equal leading dims.  One fused
+    launch (sf_attention: scores never reach memory) for 16-bit inputs with
+    D == 64 and Sk % 64 == 0; otherwise the three-launch path."""
+    d = q.shape[-1]
+    s = (1.0 / float(d) ** 0.5) if scale is None else float(scale)
+    _same_dtype(q, k, 'dev_scaled_dot_product_attention')
+    _same_dtype(q, v, 'dev_scaled_dot_product_attention')
+    if len(q.shape) < 2 or len(k.shape) != len(q.shape) or len(v.shape) != len(q.shape):
+        raise ValueError("dev_scaled_dot_product_attention: q, k, v must be (..., S, D) of equal rank")
+    if tuple(k.shape[:-2]) != tuple(q.shape[:-2]) or tuple(v.shape[:-2]) != tuple(q.shape[:-2]) \
+            or k.shape[-1] != d or v.shape[-1] != d or v.shape[-2] != k.shape[-2]:
+        raise ValueError("dev_scaled_dot_product_attention: shapes %s %s %s do not match"
+                         % (q.shape, k.shape, v.shape))
+    cdef int64_t sq = q.shape[-2]
+    cdef int64_t sk = k.shape[-2]
+    cdef int64_t batch = 1
+    for e in q.shape[:-2]:
+        batch *= e
+    if q.dtype == np.float32 or d != 64 or sk % 64 != 0:
+        return dev_sdpa_unfused(q, k, v, scale)
+    out = _alloc_like(tuple(q.shape), q.dtype, q.device_id)
+    cdef int ret
+    cdef void* pq = _ptr(q)
+    cdef void* pk = _ptr(k)
+    cdef void* pv = _ptr(v)
+    cdef void* po = _ptr(out)
+    cdef sf_dtype dt = _sf_dtype(q.dtype)
+    cdef float fs = s
+    with nogil:
+        ret = sf_attention(pq, 64, sq * 64, pk, 64, sk * 64, pv, 64, sk * 64, po, 64, sq * 64,
+                           batch, sq, sk, 64, fs, dt, NULL)
+    _check_kernel(ret)
+    return out
 
 
 # ================================================================

@@ -284,6 +284,36 @@ int sf_gemm_plan(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
   return SF_OK;
 }
 
+int sf_attention(const void* Q, int64_t ldq, int64_t strideQ, const void* K, int64_t ldk, int64_t strideK,
+                 const void* V, int64_t ldv, int64_t strideV, void* O, int64_t ldo, int64_t strideO,
+                 int64_t batch, int64_t Sq, int64_t Sk, int64_t D, float scale, sf_dtype dtype, void* stream) {
+  g_err[0] = 0;
+  if (!valid_dtype(dtype)) return fail(SF_ERR_INVALID_ARG, "sf_attention: unknown dtype %d", (int)dtype);
+  if (batch < 0 || Sq < 0 || Sk < 0 || D < 0)
+    return fail(SF_ERR_INVALID_ARG, "sf_attention: negative size");
+  if (dtype == SF_F32) return fail(SF_ERR_UNSUPPORTED, "sf_attention: 16-bit dtypes only");
+  if (D != 64) return fail(SF_ERR_UNSUPPORTED, "sf_attention: head size %lld (64 only)", (long long)D);
+  if (Sk % 64 != 0)
+    return fail(SF_ERR_UNSUPPORTED, "sf_attention: Sk=%lld is not a multiple of 64", (long long)Sk);
+  if (batch == 0 || Sq == 0) return SF_OK;
+  if (Sk == 0) return fail(SF_ERR_INVALID_ARG, "sf_attention: softmax over zero keys");
+  if (Q == nullptr || K == nullptr || V == nullptr || O == nullptr)
+    return fail(SF_ERR_INVALID_ARG, "sf_attention: null pointer");
+  if (ldq < D || ldk < D || ldv < D || ldo < D)
+    return fail(SF_ERR_INVALID_ARG, "sf_attention: row stride below the head size");
+  if (strideQ < 0 || strideK < 0 || strideV < 0 || strideO < 0)
+    return fail(SF_ERR_INVALID_ARG, "sf_attention: negative batch stride");
+  if (batch > 1 && strideO < (Sq - 1) * ldo + D)
+    return fail(SF_ERR_INVALID_ARG, "sf_attention: strideO overlaps batch entries");
+  if (Sq > INT32_MAX || Sk * (ldk > ldv ? ldk : ldv) * 2 >= (int64_t(1) << 31))
+    return fail(SF_ERR_UNSUPPORTED, "sf_attention: K/V of one batch entry must stay below 2 GiB");
+  if (!al16(Q) || !al16(K) || !al16(V) || !al16(O) || ldq % 8 || ldk % 8 || ldv % 8 || ldo % 8 ||
+      strideQ % 8 || strideK % 8 || strideV % 8 || strideO % 8)
+    return fail(SF_ERR_UNSUPPORTED, "sf_attention: rows must be 16-byte aligned");
+  return launch_attention(Q, K, V, O, batch, Sq, Sk, strideQ, strideK, strideV, strideO, ldq, ldk, ldv, ldo,
+                          scale, dtype, static_cast<hipStream_t>(stream));
+}
+
 int sf_softmax_rows(const void* x, void* y, int64_t rows, int64_t cols, sf_dtype in_dtype,
                     sf_dtype out_dtype, float scale, void* stream) {
   g_err[0] = 0;

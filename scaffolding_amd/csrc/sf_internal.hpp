@@ -42,6 +42,9 @@ int launch_gemm32(bool b_kmajor, int cfg, const GemmParams& p, int64_t batch, hi
 // Tile edge of a config (BM, BN).
 void tile_dims(int cfg, bool fp32, int& bm, int& bn);
 
+int launch_attention(const void* Q, const void* K, const void* V, void* O, int64_t batch, int64_t Sq,
+                     int64_t Sk, int64_t sQ, int64_t sK, int64_t sV, int64_t sO, int64_t ldq, int64_t ldk,
+                     int64_t ldv, int64_t ldo, float scale, sf_dtype dt, hipStream_t st);
 int launch_softmax(const void* x, void* y, int64_t rows, int64_t cols, sf_dtype in, sf_dtype out,
                    float scale, hipStream_t st);
 int launch_unary(int op, const void* x, void* y, int64_t n, sf_dtype dt, float s, hipStream_t st);

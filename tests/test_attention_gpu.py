@@ -1,0 +1,121 @@
+"""Fused attention (sf_attention) on the GPU against the fp64 closed form
+softmax(scale * q k^T) v on the quantized inputs (oracle.cpu_path.sdpa_f64),
+with the three-launch path as a second witness; ragged query counts, batch
+dims, both 16-bit dtypes, the fallback shapes and the ABI's refusals."""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from helpers import cu, rnd, up
+from oracle.configs import tol_16
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def sdpa64(q, k, v, scale):
+    """fp64 softmax(scale q k^T) v over the last two dims."""
+    q64, k64, v64 = (a.astype(np.float64) for a in (q, k, v))
+    s = scale * (q64 @ np.swapaxes(k64, -1, -2))
+    s -= s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=-1, keepdims=True)
+    return p @ v64
+
+
+def down(gt):
+    return cu().gputensor_to_numpy(gt).astype(np.float32)
+
+
+EPS = {"float16": 2.0 ** -11, "bfloat16": 2.0 ** -8}
+
+
+def bound(q, k, v, scale, dtype, unfused=False):
+    """BASELINE's 16-bit tolerance at K = Sk plus the rounding this op adds
+    beyond one GEMM: P rounded to the input dtype (relative eps each, moving
+    o by <= eps * max|v|), the output rounding (<= eps * max|o| <= eps *
+    max|v|), and on the three-launch path the scores rounded before the
+    softmax (|d p| <= p * 2 eps |s|, so <= 2 eps max|s| max|v|)."""
+    eps = EPS[dtype]
+    vmax = float(np.max(np.abs(v)))
+    b = tol_16(k.shape[-2]) + 2 * eps * vmax
+    if unfused:
+        smax = float(np.max(np.abs(scale * (q.astype(np.float64) @ np.swapaxes(k.astype(np.float64), -1, -2)))))
+        b += 2 * eps * smax * vmax
+    return b
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("shape", [(1, 256, 64), (3, 300, 128), (2, 17, 320), (4, 513, 64)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_fused_attention_matches_fp64(dtype, shape):
+    b, sq, sk = shape
+    rng = np.random.default_rng(sq + 7 * sk + b)
+    q = rnd(rng, (b, sq, 64), 1.0, dtype)
+    k = rnd(rng, (b, sk, 64), 1.0, dtype)
+    v = rnd(rng, (b, sk, 64), 1.0, dtype)
+    scale = 0.125
+    g = cu()
+    gq, gk, gv = up(q, dtype), up(k, dtype), up(v, dtype)
+    o = down(g.dev_scaled_dot_product_attention(gq, gk, gv, scale))
+    o64 = sdpa64(q, k, v, scale)
+    err = float(np.max(np.abs(o - o64)))
+    assert err <= bound(q, k, v, scale, dtype), err
+    # the three-launch path agrees to its own bound
+    o3 = down(g.dev_sdpa_unfused(gq, gk, gv, scale))
+    err3 = float(np.max(np.abs(o3 - o64)))
+    assert err3 <= bound(q, k, v, scale, dtype, unfused=True), err3
+
+
+def test_fused_attention_large_scores_and_leading_dims():
+    """Scores of magnitude ~50 (exp2 range, running-max correction across
+    key blocks: the maximum sits in a late block) and (2, 3, S, 64) inputs."""
+    rng = np.random.default_rng(9)
+    q = rnd(rng, (2, 3, 130, 64), 1.0, "float16")
+    k = rnd(rng, (2, 3, 192, 64), 1.0, "float16")
+    k[:, :, 150] = q[:, :, 0:1].mean(axis=2) * 6  # one late key dominates some rows
+    k = k.astype(np.float16).astype(np.float32)
+    v = rnd(rng, (2, 3, 192, 64), 1.0, "float16")
+    g = cu()
+    o = down(g.dev_scaled_dot_product_attention(up(q, "float16"), up(k, "float16"), up(v, "float16"), 1.0))
+    o64 = sdpa64(q, k, v, 1.0)
+    assert o.shape == (2, 3, 130, 64)
+    assert np.all(np.isfinite(o))
+    assert float(np.max(np.abs(o - o64))) <= bound(q, k, v, 1.0, "float16")
+
+
+@pytest.mark.parametrize("shape", [(2, 40, 100, 64), (1, 64, 64, 32), (1, 33, 128, 80)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_unsupported_shapes_fall_back(shape):
+    b, sq, sk, d = shape
+    rng = np.random.default_rng(3)
+    q = rnd(rng, (b, sq, d), 1.0, "bfloat16")
+    k = rnd(rng, (b, sk, d), 1.0, "bfloat16")
+    v = rnd(rng, (b, sk, d), 1.0, "bfloat16")
+    g = cu()
+    o = down(g.dev_scaled_dot_product_attention(up(q, "bfloat16"), up(k, "bfloat16"), up(v, "bfloat16"), None))
+    o64 = sdpa64(q, k, v, 1.0 / np.sqrt(d))
+    assert float(np.max(np.abs(o - o64))) <= bound(q, k, v, 1.0 / np.sqrt(d), "bfloat16", unfused=True)
+
+
+def test_abi_refusals():
+    so = ctypes.CDLL(os.path.join(ROOT, "scaffolding_amd", "libsfgemm.so"))
+    so.sf_last_error.restype = ctypes.c_char_p
+    I64, P = ctypes.c_int64, ctypes.c_void_p
+    x = up(np.zeros((1, 64, 64), np.float32), "float16")
+    p = P(x.data_ptr)
+
+    def call(d=64, sk=64, dt=1, ld=64):
+        return so.sf_attention(p, I64(ld), I64(0), p, I64(ld), I64(0), p, I64(ld), I64(0), p, I64(ld), I64(0),
+                               I64(1), I64(64), I64(sk), I64(d), ctypes.c_float(1.0), dt, None)
+    assert call() == 0
+    assert call(d=32) == -3 and b"head size" in so.sf_last_error()
+    assert call(sk=96) == -3 and b"multiple of 64" in so.sf_last_error()
+    assert call(dt=0) == -3 and b"16-bit" in so.sf_last_error()
+    assert call(ld=63) == -2
+    cu().device_synchronize()

@@ -101,14 +101,17 @@ def test_c4_attention_fp16():
     sums = probs.astype(np.float64).sum(axis=-1)
     assert np.all(np.abs(sums - 1.0) <= s * 2.0 ** -11 * (1.0 / s) * 4 + 2e-3), float(np.max(np.abs(sums - 1)))
     del probs, gp
-    # end-to-end SDPA output against fp64 softmax(scale q k^T) v
-    go = g.dev_scaled_dot_product_attention(gq, gk, gv, scale)
-    assert go.shape == (bh, s, d) and go.dtype == np.float16
-    o = g.gputensor_to_numpy(go).astype(np.float32)
-    for h in heads:
-        o64 = ref.sdpa_f64(q[h:h + 1, rows], k[h:h + 1], v[h:h + 1], scale)[0]
-        err = cfg.abs_err(o[h, rows], o64)
-        assert err <= cfg.tol_16(s), (h, err)
+    # end-to-end SDPA output against fp64 softmax(scale q k^T) v: the
+    # three-launch path and the fused kernel
+    for fn in (g.dev_sdpa_unfused, g.dev_scaled_dot_product_attention):
+        go = fn(gq, gk, gv, scale)
+        assert go.shape == (bh, s, d) and go.dtype == np.float16
+        o = g.gputensor_to_numpy(go).astype(np.float32)
+        del go
+        for h in heads:
+            o64 = ref.sdpa_f64(q[h:h + 1, rows], k[h:h + 1], v[h:h + 1], scale)[0]
+            err = cfg.abs_err(o[h, rows], o64)
+            assert err <= cfg.tol_16(s), (fn.__name__, h, err)
 
 
 @pytest.mark.parametrize("proj", list(cfg.C5_PROJ))
