@@ -1,0 +1,281 @@
+// attention.hpp — fused scaled-dot-product attention forward for head size
+// 64, 16-bit Q/K/V/O with fp32 accumulation:
+//
+//   O[b] = softmax(scale * Q[b] K[b]^T) V[b],  Q [Sq, 64], K, V [Sk, 64].
+//
+// One 256-thread workgroup per 256 query rows of one batch entry; wave w
+// owns 64 of them (four 16-row blocks); at most 256 registers per lane, so
+// two workgroups share a CU.  The workgroup streams K and V in blocks of 64
+// keys through a 3-stage LDS ring (16 KB per stage, loaded two blocks
+// ahead), and per block each wave
+//   1. forms S = Q K^T for its 64 x 64 scores: 32 v_mfma_f32_16x16x32 with
+//      Q fragments held in registers for the whole loop and K fragments
+//      read from LDS (ds_read_b128, 128-byte lines, chunk h at slot
+//      h ^ (row & 7), conflict-free as in the GEMM kernels);
+//   2. keeps the softmax in the exp2 domain against a per-row reference m
+//      that is raised lazily: only when a score exceeds m + 8 does the wave
+//      reduce the row maxima across the four lanes sharing a row and scale
+//      O and the row sums by 2^(m_old - m_new), so P = 2^(S scale log2 e - m)
+//      stays <= 2^8 and the common path needs no cross-lane traffic;
+//   3. packs P to 16 bits (v_cvt_pk) and adds P V into the 64 x 64 fp32 O
+//      accumulator (32 MFMAs, V fragments from ds_read_b64_tr_b16, gfx950's
+//      transposing LDS read) and P 1 into the row sums (8 MFMAs against a
+//      fragment of ones, so the sums use the same rounded P as O).
+// P's MFMA k slots follow the score accumulator layout (lane group g holds
+// keys 4g..4g+3 and 16+4g..16+4g+3 of each 32-key chunk), and the V
+// fragment reads use the same key order, so P never moves between lanes.
+// The 2 GB score and probability tensors of the three-kernel path are never
+// written.  Requires head size 64, Sk % 64 == 0, 16-byte aligned rows.
+#pragma once
+
+#include "gemm16nt_pp.hpp"
+
+namespace sf {
+
+struct AttnParams {
+  const void* Q;
+  const void* K;
+  const void* V;
+  void* O;
+  int64_t sQ, sK, sV, sO;      // batch strides, elements
+  int ldq, ldk, ldv, ldo;      // row strides, elements
+  int Sq, Sk;
+  float scale_log2e;           // scale * log2(e)
+};
+
+// ds_read_b64_tr_b16 as inline assembly (see ds_read16 for why): within each
+// 16-lane group, lane 4a + b receives element b of the 8-byte rows addressed
+// by lanes a, 4 + a, 8 + a and 12 + a (measured lane layout).
+template <int OFF>
+__device__ __forceinline__ u32x2 ds_read_tr16(uint32_t addr) {
+  u32x2 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+template <typename T>
+__global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
+  constexpr int NS = 3;
+  constexpr int KB = 64;
+  constexpr int BLK = KB * 128;
+  constexpr float THRESH = 8.0f;
+  __shared__ __attribute__((aligned(1024))) uint8_t sK[NS][BLK];
+  __shared__ __attribute__((aligned(1024))) uint8_t sV[NS][BLK];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b = blockIdx.y;
+  const int q0 = blockIdx.x * 256 + wave * 64;
+  const int Sq = p.Sq, Sk = p.Sk;
+  const int NB = Sk / KB;
+  const uint16_t* Qb = static_cast<const uint16_t*>(p.Q) + b * p.sQ;
+  const uint16_t* Kb = static_cast<const uint16_t*>(p.K) + b * p.sK;
+  const uint16_t* Vb = static_cast<const uint16_t*>(p.V) + b * p.sV;
+
+  const __amdgpu_buffer_rsrc_t rK =
+      __builtin_amdgcn_make_buffer_rsrc((void*)Kb, (short)0, (int)((uint32_t)Sk * (uint32_t)p.ldk * 2u), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rV =
+      __builtin_amdgcn_make_buffer_rsrc((void*)Vb, (short)0, (int)((uint32_t)Sk * (uint32_t)p.ldv * 2u), 0x00020000);
+  const int drow = wave * 16 + (lane >> 3);
+  const uint32_t dch = (uint32_t)(((lane & 7) ^ (lane >> 3)) * 16);
+  const uint32_t vk0 = (uint32_t)drow * (uint32_t)p.ldk * 2u + dch;
+  const uint32_t vv0 = (uint32_t)drow * (uint32_t)p.ldv * 2u + dch;
+  const uint32_t k8 = 8u * (uint32_t)p.ldk * 2u, v8 = 8u * (uint32_t)p.ldv * 2u;
+  auto issue = [&](int j) {
+    const int s = j % NS;
+    const int ko = j * KB * p.ldk * 2, vo = j * KB * p.ldv * 2;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rK, (lds_ptr_t)(&sK[s][0] + wave * 2048), 16, vk0, ko, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rK, (lds_ptr_t)(&sK[s][0] + wave * 2048 + 1024), 16, vk0 + k8, ko, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rV, (lds_ptr_t)(&sV[s][0] + wave * 2048), 16, vv0, vo, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rV, (lds_ptr_t)(&sV[s][0] + wave * 2048 + 1024), 16, vv0 + v8, vo, 0, 0);
+  };
+  issue(0);
+  if (NB > 1) issue(1);
+
+  u32x4 qf[4][2];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    int r = q0 + mb * 16 + (lane & 15);
+    r = r < Sq ? r : Sq - 1;
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc)
+      qf[mb][kc] = *reinterpret_cast<const u32x4*>(Qb + (int64_t)r * p.ldq + kc * 32 + 8 * (lane >> 4));
+  }
+
+  f32x4 o[4][4], osum[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    osum[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o[mb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  float mrow[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) mrow[mb] = -INFINITY;
+  const float sc = p.scale_log2e;
+  // 16-bit 1.0 in both halves of every dword: the X fragment of a ones block.
+  const uint32_t one2 = (uint32_t)Elem<T>::from_f32(1.0f) * 0x10001u;
+  const u32x4 ones = u32x4{one2, one2, one2, one2};
+
+  const uint32_t kfo = (uint32_t)((lane & 15) * 128 + (((lane >> 4) ^ (lane & 7)) << 4));
+  const int vs = lane & 15, vg = lane >> 4;
+  const int vrow0 = 4 * vg + (vs >> 2);
+  const uint32_t vfo_base = (uint32_t)vrow0 * 128u + (uint32_t)((vs & 1) * 8);
+  const int vch = (vs & 3) >> 1;
+  const int vsw = vrow0 & 7;
+
+  for (int j = 0; j < NB; ++j) {
+    const int st = j % NS;
+    __builtin_amdgcn_sched_barrier(0);
+    if (j + 1 < NB)
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, 0));
+    else
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    if (j + 2 < NB) issue(j + 2);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- S = Q K^T, K fragments per 16-key block ------------------------
+    const uint32_t ka = lds_addr(&sK[st][0]) + kfo;
+    f32x4 s[4][4];
+    u32x4 kf0 = ds_read16<0>(ka), kf1 = ds_read16<0>(ka ^ 64);
+    static_for<4>([&](auto nbc) {
+      constexpr int NBK = decltype(nbc)::value;
+      u32x4 nk0, nk1;
+      if constexpr (NBK < 3) {
+        nk0 = ds_read16<(NBK + 1) * 2048>(ka);
+        nk1 = ds_read16<(NBK + 1) * 2048>(ka ^ 64);
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 2));  // this block's pair landed
+      } else {
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // Independent chains back to back: all kc = 0 products, then kc = 1.
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) s[mb][NBK] = Mfma16<T>::run(kf0, qf[mb][0], f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) s[mb][NBK] = Mfma16<T>::run(kf1, qf[mb][1], s[mb][NBK]);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (NBK < 3) {
+        kf0 = nk0;
+        kf1 = nk1;
+      }
+    });
+
+    // ---- online softmax with lazy rescale --------------------------------
+    // Each lane checks its 16 scores of each row against the row's current
+    // reference m; only if some score exceeds m + THRESH (log2 units) does
+    // the wave reduce the row maxima across the four lanes of each row and
+    // rescale O and the row sums.  Otherwise 2^(s sc - m) <= 2^THRESH.
+    float lmax[4];
+    bool need = false;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      float mx = fmaxf(fmaxf(s[mb][0][0], s[mb][0][1]), s[mb][0][2]);
+      mx = fmaxf(fmaxf(mx, s[mb][0][3]), s[mb][1][0]);
+      mx = fmaxf(fmaxf(mx, s[mb][1][1]), s[mb][1][2]);
+      mx = fmaxf(fmaxf(mx, s[mb][1][3]), s[mb][2][0]);
+      mx = fmaxf(fmaxf(mx, s[mb][2][1]), s[mb][2][2]);
+      mx = fmaxf(fmaxf(mx, s[mb][2][3]), s[mb][3][0]);
+      mx = fmaxf(fmaxf(mx, s[mb][3][1]), s[mb][3][2]);
+      mx = fmaxf(mx, s[mb][3][3]);
+      lmax[mb] = mx * sc;
+      need |= lmax[mb] > mrow[mb] + THRESH;
+    }
+    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        float mx = lmax[mb];
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mnew = fmaxf(mrow[mb], mx);
+        const float corr = __builtin_amdgcn_exp2f(mrow[mb] - mnew);
+        mrow[mb] = mnew;
+        osum[mb] *= corr;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) o[mb][db] *= corr;
+      }
+    }
+    u32x4 pf[4][2];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const float nm = -mrow[mb];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        uint32_t w[4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int q2 = 0; q2 < 2; ++q2) {
+            const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[mb][2 * c + h][2 * q2], sc, nm));
+            const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[mb][2 * c + h][2 * q2 + 1], sc, nm));
+            w[h * 2 + q2] = pack2<T>(e0, e1);
+          }
+        pf[mb][c] = u32x4{w[0], w[1], w[2], w[3]};
+      }
+    }
+
+    // ---- O += P V, V fragments per 16-d block; row sums against ones ------
+    const uint32_t va = lds_addr(&sV[st][0]) + vfo_base;
+    auto vread = [&](int db, u32x4& f0, u32x4& f1) {
+      const uint32_t a0 = va + (uint32_t)(((2 * db + vch) ^ vsw) << 4);
+      const u32x2 t00 = ds_read_tr16<0>(a0);
+      const u32x2 t01 = ds_read_tr16<16 * 128>(a0);
+      const u32x2 t10 = ds_read_tr16<32 * 128>(a0);
+      const u32x2 t11 = ds_read_tr16<48 * 128>(a0);
+      f0 = u32x4{t00.x, t00.y, t01.x, t01.y};
+      f1 = u32x4{t10.x, t10.y, t11.x, t11.y};
+    };
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 vf0, vf1;
+    vread(0, vf0, vf1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) osum[mb] = Mfma16<T>::run(ones, pf[mb][0], osum[mb]);
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) osum[mb] = Mfma16<T>::run(ones, pf[mb][1], osum[mb]);
+    static_for<4>([&](auto dbc) {
+      constexpr int DB = decltype(dbc)::value;
+      u32x4 nv0, nv1;
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (DB < 3) {
+        vread(DB + 1, nv0, nv1);
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 4));
+      } else {
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) o[mb][DB] = Mfma16<T>::run(vf0, pf[mb][0], o[mb][DB]);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) o[mb][DB] = Mfma16<T>::run(vf1, pf[mb][1], o[mb][DB]);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (DB < 3) {
+        vf0 = nv0;
+        vf1 = nv1;
+      }
+    });
+  }
+
+  uint16_t* Ob = static_cast<uint16_t*>(p.O) + b * p.sO;
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    const float inv = 1.0f / osum[mb][0];
+    const int r = q0 + mb * 16 + (lane & 15);
+    if (r < Sq) {
+      uint16_t* orow = Ob + (int64_t)r * p.ldo;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const int d = db * 16 + 4 * (lane >> 4);
+        const uint32_t lo = pack2<T>(o[mb][db][0] * inv, o[mb][db][1] * inv);
+        const uint32_t hi = pack2<T>(o[mb][db][2] * inv, o[mb][db][3] * inv);
+        *reinterpret_cast<u32x2*>(orow + d) = u32x2{lo, hi};
+      }
+    }
+  }
+}
+
+}  // namespace sf

@@ -104,6 +104,23 @@ __device__ __forceinline__ float act_t(float v) {
     return v;
 }
 
+// Two fp32 values rounded (RNE) to the 16-bit type T and packed, a in the
+// low half: one v_cvt_pk_{f16,bf16}_f32.
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float a, float b);
+template <>
+__device__ __forceinline__ uint32_t pack2<F16>(float a, float b) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, h2));
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<BF16>(float a, float b) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, b2));
+}
+
 // static_for<N>(f): f(std::integral_constant<int, 0>{}) ... f(..., N - 1>{})
 // in order, each index a compile-time constant.
 template <int N>
