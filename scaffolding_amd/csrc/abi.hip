@@ -70,6 +70,9 @@ int launch_gemm16(sf_dtype in, sf_dtype out, bool b_kmajor, int cfg, const GemmP
   unsigned gx;
   if (cfg == TILE_SKINNY)
     gx = static_cast<unsigned>((p.N + 31) / 32);
+  else if (p.split > 0)
+    gx = static_cast<unsigned>(p.full_tiles) +
+         static_cast<unsigned>(p.tiles_m * p.tiles_n - p.full_tiles) * static_cast<unsigned>(p.split);
   else
     gx = static_cast<unsigned>(p.tiles_m) * static_cast<unsigned>(p.tiles_n);
   for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
@@ -129,6 +132,79 @@ static int choose_tile32(int64_t M, int64_t N, int64_t batch, bool vec, int cus)
   if (!vec) return TILE_GENERIC;
   if (cdiv(M, 128) * cdiv(N, 128) * batch >= cus) return TILE_128x128;
   return TILE_64x64;
+}
+
+// ---------------------------------------------------------------------
+// Per-device workspace of the split-tail GEMM: fp32 partial tiles and one
+// counter per split tile.  Counters start at zero (cleared by a kernel when
+// the buffer is created) and every split tile's last part resets its own,
+// so the buffer is ready for the next launch.  Launches on one stream are
+// ordered by the stream; a launch on another stream first waits for the
+// event recorded after the previous split launch.  Growing the buffer
+// synchronises the device before freeing the old one.
+// ---------------------------------------------------------------------
+struct SplitWorkspace {
+  void* base = nullptr;
+  size_t part_bytes = 0;
+  int counters = 0;
+  hipEvent_t done = nullptr;
+  hipStream_t last = nullptr;
+  bool used = false;
+};
+static std::mutex g_ws_mu;
+static std::unordered_map<int, SplitWorkspace> g_ws;
+
+static int split_workspace_acquire(size_t part_bytes, int ncounters, hipStream_t st, float** ws, int** cnt) {
+  int dev = 0;
+  int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (rc != SF_OK) return rc;
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  SplitWorkspace& w = g_ws[dev];
+  if (w.done == nullptr) {
+    rc = check_hip(hipEventCreateWithFlags(&w.done, hipEventDisableTiming), "hipEventCreate (split workspace)");
+    if (rc != SF_OK) return rc;
+  }
+  if (part_bytes > w.part_bytes || ncounters > w.counters) {
+    const size_t pb = part_bytes > w.part_bytes ? part_bytes : w.part_bytes;
+    const int nc = ncounters > w.counters ? ncounters : w.counters;
+    if (w.base != nullptr) {
+      rc = check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize (split workspace)");
+      if (rc != SF_OK) return rc;
+      (void)hipFree(w.base);
+      w.base = nullptr;
+      w.part_bytes = 0;
+      w.counters = 0;
+    }
+    void* p = nullptr;
+    rc = check_hip(hipMalloc(&p, pb + (size_t)nc * sizeof(int)), "hipMalloc (split workspace)");
+    if (rc != SF_OK) return rc;
+    rc = launch_zero(static_cast<uint8_t*>(p) + pb, (size_t)nc * sizeof(int), st);
+    if (rc != SF_OK) {
+      (void)hipFree(p);
+      return rc;
+    }
+    w.base = p;
+    w.part_bytes = pb;
+    w.counters = nc;
+    w.used = false;
+  } else if (w.used && w.last != st) {
+    rc = check_hip(hipStreamWaitEvent(st, w.done, 0), "hipStreamWaitEvent (split workspace)");
+    if (rc != SF_OK) return rc;
+  }
+  *ws = static_cast<float*>(w.base);
+  *cnt = reinterpret_cast<int*>(static_cast<uint8_t*>(w.base) + w.part_bytes);
+  return SF_OK;
+}
+
+static int split_workspace_release(hipStream_t st) {
+  int dev = 0;
+  int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (rc != SF_OK) return rc;
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  SplitWorkspace& w = g_ws[dev];
+  w.last = st;
+  w.used = true;
+  return check_hip(hipEventRecord(w.done, st), "hipEventRecord (split workspace)");
 }
 
 static bool valid_dtype(int d) { return d == SF_F32 || d == SF_F16 || d == SF_BF16; }
@@ -244,6 +320,25 @@ static int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K,
   p.tiles_m = (int)cdiv(M, bm);
   p.tiles_n = (int)cdiv(N, bn);
   p.rows_per = 0;
+  p.full_tiles = 0;
+  p.split = 0;
+  p.ws = nullptr;
+  p.counters = nullptr;
+  if (plan.cfg == TILE_NT_BIG && batch == 1 && K % 128 == 0) {
+    // Tail split: with R = tiles % CUs left over after whole waves, run the
+    // last R tiles as R * s workgroups of K / s each (s <= CUs / R), so the
+    // last wave is full instead of R / CUs full.
+    const int64_t T = (int64_t)p.tiles_m * p.tiles_n, R = T % cus, units = K / 128;
+    if (R > 0 && 2 * R <= cus && units >= 2) {
+      int64_t sp = cus / R;
+      if (sp > units) sp = units;
+      if (sp > 8) sp = 8;
+      if (sp >= 2) {
+        p.full_tiles = (int)(T - R);
+        p.split = (int)sp;
+      }
+    }
+  }
   if (plan.cfg == TILE_SKINNY_LINE) {
     // One workgroup per CU where N allows, at most 64 rows of W each.
     int64_t rp = cdiv(N, cus);
@@ -265,6 +360,15 @@ int sf_gemm(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t bat
   if (rc != SF_OK || plan.noop) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (plan.fp32) return launch_gemm32(plan.b_kmajor, plan.cfg, plan.p, batch, st);
+  if (plan.p.split > 0) {
+    const int nsplit = plan.p.tiles_m * plan.p.tiles_n - plan.p.full_tiles;
+    rc = split_workspace_acquire((size_t)nsplit * plan.p.split * (256u * 256u * 4u), nsplit, st, &plan.p.ws,
+                                 &plan.p.counters);
+    if (rc != SF_OK) return rc;
+    rc = launch_gemm16(ab_dtype, c_dtype, plan.b_kmajor, plan.cfg, plan.p, batch, st);
+    const int rc2 = split_workspace_release(st);
+    return rc != SF_OK ? rc : rc2;
+  }
   return launch_gemm16(ab_dtype, c_dtype, plan.b_kmajor, plan.cfg, plan.p, batch, st);
 }
 
@@ -279,8 +383,12 @@ int sf_gemm_plan(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
   int rc = gemm_prepare(transA, transB, M, N, K, batch, A, lda, strideA, B, ldb, strideB, C, ldc,
                         strideC, ab_dtype, c_dtype, alpha, bias, epi, false, plan);
   if (rc != SF_OK) return rc;
-  snprintf(buf, (size_t)len, "%s%s", plan.noop ? "noop" : tile_name(plan.cfg),
-           plan.noop ? "" : (plan.fp32 ? " fp32" : " 16-bit"));
+  char extra[48] = "";
+  if (!plan.noop && plan.p.split > 0)
+    snprintf(extra, sizeof(extra), " split-tail %dx%d", plan.p.tiles_m * plan.p.tiles_n - plan.p.full_tiles,
+             plan.p.split);
+  snprintf(buf, (size_t)len, "%s%s%s", plan.noop ? "noop" : tile_name(plan.cfg),
+           plan.noop ? "" : (plan.fp32 ? " fp32" : " 16-bit"), extra);
   return SF_OK;
 }
 

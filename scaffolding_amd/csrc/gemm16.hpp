@@ -50,6 +50,14 @@ struct GemmParams {
   int epi;  // sf_epilogue
   int tiles_m, tiles_n;
   int rows_per;  // skinny line kernel: W rows per workgroup
+  // Split tail of the 256 x 256 NT kernel (batch 1): tiles [0, full_tiles)
+  // run whole; each later tile is split over k into `split` parts whose
+  // fp32 partial tiles go to `ws` (256 KB each) and are summed, in part
+  // order, by the part that finishes last (`counters`: one per split tile,
+  // zero between launches).  split == 0: no tail split.
+  int full_tiles, split;
+  float* ws;
+  int* counters;
 };
 
 template <typename T> struct Mfma16;
@@ -75,14 +83,12 @@ __device__ __forceinline__ int swz(int row, int chunk) {
 template <typename TOut> struct Store4 {  // 16-bit outputs
   __device__ __forceinline__ static void run(uint16_t* crow, int n, int N, bool vec_ok,
                                              const float v[4]) {
-    uint16_t h[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) h[q] = Elem<TOut>::from_f32(v[q]);
     if (vec_ok && n + 3 < N) {
-      u32x2 o = {static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16),
-                 static_cast<uint32_t>(h[2]) | (static_cast<uint32_t>(h[3]) << 16)};
-      *reinterpret_cast<u32x2*>(crow + n) = o;
+      *reinterpret_cast<u32x2*>(crow + n) = u32x2{pack2<TOut>(v[0], v[1]), pack2<TOut>(v[2], v[3])};
     } else {
+      uint16_t h[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) h[q] = Elem<TOut>::from_f32(v[q]);
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         if (n + q < N) crow[n + q] = h[q];

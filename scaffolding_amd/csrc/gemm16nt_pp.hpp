@@ -68,6 +68,30 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
+// 16-byte global store with the sc0 sc1 cache-policy bits: the agent-scope
+// coherent form the compiler emits for relaxed agent-scope atomic stores
+// (visible across the XCDs' separate L2s once complete), four times wider.
+// Completion is ordered by the caller's s_waitcnt vmcnt(0).
+__device__ __forceinline__ void store16_coherent(float* p, f32x4 v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
+}
+
+// 16-byte coherent global load (sc0 sc1) issued without waiting; the caller
+// must pass the result through wait_vm0_tie8 before using it.
+__device__ __forceinline__ f32x4 load16_coherent_nowait(const float* p) {
+  f32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off sc0 sc1" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+// s_waitcnt vmcnt(0) that the eight loaded values depend on, so no use of
+// them is scheduled above the wait.
+__device__ __forceinline__ void wait_vm0_tie8(f32x4 (&v)[8]) {
+  asm volatile("s_waitcnt vmcnt(0)"
+               : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7])
+               :
+               : "memory");
+}
+
 // s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] |
 // lgkmcnt[11:8] | vmcnt[5:4] << 14); counts not being waited on are at max.
 constexpr int waitcnt_imm(int vm, int lgkm) {
@@ -94,9 +118,40 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   const int wm = wave >> 2;
   const int wn = wave & 3;
 
+  const int M = p.M, N = p.N, K = p.K;
   int tm, tn;
+  // This workgroup's k slices [t_begin, t_begin + KT) and, in a split tile,
+  // its part index (-1: whole tile).
+  int t_begin = 0, KT = K / BK, part = -1, split_tile = 0;
   {
-    int pid = xcd_remap(blockIdx.x, gridDim.x);
+    int pid;
+    int spid = -1;  // split part id
+    if (NSTAGE == 2 && p.split > 0) {
+      // Every XCD gets the same share of whole tiles (a contiguous range, as
+      // xcd_remap gives) followed by its share of split parts, so the XCDs
+      // finish together; within an XCD the long jobs are dispatched first.
+      const int xcd = blockIdx.x % kNumXcd, o = blockIdx.x / kNumXcd;
+      const int fx = p.full_tiles / kNumXcd;  // full_tiles is a multiple of the CU count
+      const int P = (p.tiles_m * p.tiles_n - p.full_tiles) * p.split;
+      if (o < fx) {
+        pid = xcd * fx + o;
+      } else {
+        spid = xcd * (P / kNumXcd) + (xcd < P % kNumXcd ? xcd : P % kNumXcd) + (o - fx);
+        pid = p.full_tiles + spid / p.split;
+      }
+    } else {
+      pid = xcd_remap(blockIdx.x, gridDim.x);
+    }
+    if (spid >= 0) {
+      const int r = spid / p.split, q = spid % p.split;
+      const int units = K / (4 * BK);  // 128-k units
+      const int u0 = q * units / p.split, u1 = (q + 1) * units / p.split;
+      t_begin = 4 * u0;
+      KT = 4 * (u1 - u0);
+      part = q;
+      split_tile = r;
+      pid = p.full_tiles + r;
+    }
     group_tile(pid, p.tiles_m, p.tiles_n, 8, tm, tn);
   }
   const int m0 = tm * BM;
@@ -104,9 +159,7 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   const int64_t b = blockIdx.y;
   const uint16_t* __restrict__ A = static_cast<const uint16_t*>(p.A) + b * p.sA;
   const uint16_t* __restrict__ B = static_cast<const uint16_t*>(p.B) + b * p.sB;
-  const int M = p.M, N = p.N, K = p.K;
-  const int KT = K / BK;  // multiple of 4
-  const int KP = KT / 2;  // slice pairs
+  const int KP = KT / 2;  // slice pairs (KT a multiple of 4)
 
   // A pair stage holds 64 k-columns: line r (128 B) is row r's 64 k values,
   // logical 16-byte chunk h (k = 8h .. 8h+7) at slot h ^ (r & 7).  Slice 2s
@@ -132,7 +185,7 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
     vob[i] = (uint32_t)(gb < N ? gb : N - 1) * (uint32_t)p.ldb * 2u + dchunk_b;
   }
   auto dma = [&](uint8_t* sA, uint8_t* sB, int k0) {
-    const int so = k0 * 2;
+    const int so = (t_begin * BK + k0) * 2;
 #pragma unroll
     for (int i = 0; i < DMA_I; ++i) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_ptr_t)(sA + (wave * 32 + i * 8) * 128), 16, voa[i], so, 0, 0);
@@ -209,6 +262,58 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   if (grp == 0) __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
 
+  // ---- split tile: park the partial, the last part sums all of them ---------
+  // Partials move with agent-scope coherent stores (sc0 sc1, 16 bytes) and
+  // relaxed agent-scope atomic loads: coherent across the XCDs' separate L2s
+  // without the whole-L2 writeback and invalidate a device-scope fence costs.  Each thread waits for its own stores to
+  // complete (vmcnt 0) before the workgroup barrier that precedes the
+  // counter increment, so the part that sees count split - 1 reads every
+  // other part's data from memory.
+  if (NSTAGE == 2 && part >= 0) {
+    const int tid = threadIdx.x;
+    float* mine = p.ws + (size_t)(split_tile * p.split + part) * (FN * FM * 512 * 4);
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+        store16_coherent(mine + (size_t)((i * FM + j) * 512 + tid) * 4, acc[i][j]);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    __shared__ int arrived;
+    if (tid == 0)
+      arrived = __hip_atomic_fetch_add(&p.counters[split_tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (arrived != p.split - 1) return;  // workgroup-uniform
+    // Sum the parts in part order (the same bits whichever part is last),
+    // one B block (8 fragments, 8 coherent 16-byte loads in flight) per
+    // round trip.
+    const float* all = p.ws + (size_t)split_tile * p.split * (FN * FM * 512 * 4);
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+      f32x4 sum[FM];
+#pragma unroll
+      for (int j = 0; j < FM; ++j) sum[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int q = 0; q < p.split; ++q) {
+        if (q == part) {
+#pragma unroll
+          for (int j = 0; j < FM; ++j) sum[j] += acc[i][j];
+        } else {
+          const float* src = all + ((size_t)q * (FN * FM) + i * FM) * 512 * 4 + (size_t)tid * 4;
+          f32x4 v[FM];
+#pragma unroll
+          for (int j = 0; j < FM; ++j) v[j] = load16_coherent_nowait(src + (size_t)j * 512 * 4);
+          wait_vm0_tie8(v);
+#pragma unroll
+          for (int j = 0; j < FM; ++j) sum[j] += v[j];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < FM; ++j) acc[i][j] = sum[j];
+    }
+    if (tid == 0) __hip_atomic_store(&p.counters[split_tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+  }
+
   // ---- epilogue ------------------------------------------------------------
   const bool has_bias = epi_has_bias(p.epi);
   const int act = epi_act(p.epi);
@@ -252,8 +357,8 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
         float v[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[q] = act_t<ACT>(acc[i][j][q] * alpha + bv[i][q]);
-        const uint32_t lo = Elem<TOut>::from_f32(v[0]) | ((uint32_t)Elem<TOut>::from_f32(v[1]) << 16);
-        const uint32_t hi = Elem<TOut>::from_f32(v[2]) | ((uint32_t)Elem<TOut>::from_f32(v[3]) << 16);
+        const uint32_t lo = pack2<TOut>(v[0], v[1]);
+        const uint32_t hi = pack2<TOut>(v[2], v[3]);
         *reinterpret_cast<u32x2*>(stage + r * PITCH + (i * 16 + 4 * (lane >> 4)) * 2) = u32x2{lo, hi};
       }
     }

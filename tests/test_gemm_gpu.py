@@ -260,6 +260,47 @@ def test_skinny_line_fp32_output():
     check_bound(y, y64, gemm_bound(y64, absprod, k, "float32"), "skinny line fp32 out")
 
 
+SPLIT_CASES = [
+    # (M, N, K, act, bias, expected "split-tail R x s")
+    (4352, 4096, 1024, None, False, "split-tail 16x8"),    # 272 tiles: 16 left over, 8 parts of 128 k
+    (7900, 2800, 896, "gelu", True, "split-tail 85x3"),   # 341 tiles: 85 left, 7 units in 3 uneven parts
+    (17776, 1920, 1920, None, True, "split-tail 48x5"),   # C5 out-projection shape
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: "%dx%dx%d" % c[:3])
+def test_split_tail_linear(case):
+    """The 256x256 NT kernel with its last partial wave of tiles split over k:
+    fp32 partials in a workspace, summed in part order by the last part.
+    Two launches in a row check that the per-tile counters reset; sampled
+    rows (including every split tile's rows) against fp64, checksums over all."""
+    m, n, k, act, bias, expect = case
+    rng = np.random.default_rng(m + n + k)
+    x = rnd(rng, (m, k), 1.0, "bfloat16")
+    w = rnd(rng, (n, k), 1.0 / np.sqrt(k), "bfloat16")
+    b = rnd(rng, (n,), 0.5, "bfloat16") if bias else None
+    gx, gw = up(x, "bfloat16"), up(w, "bfloat16")
+    gb = up(b, "bfloat16") if bias else None
+    plan = cu().gemm_plan(1, m, n, k, 1, gx.data_ptr, k, 0, gw.data_ptr, k, 0, n, 0, gx.dtype,
+                          epi=1 if bias else 0, ptr_bias=gb.data_ptr if bias else 0)
+    assert plan.startswith("gemm nt 256x256 lds-dma") and expect in plan, plan
+    y1 = down(cu().dev_linear_forward(gx, gw, gb, act))
+    y2 = down(cu().dev_linear_forward(gx, gw, gb, act))
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32)), "split tail not deterministic"
+    # rows of the last tile rows (where split tiles sit in tile order) and a sample
+    rows = np.unique(np.r_[0, m - 1, np.arange(0, m, 131), np.arange(max(0, m - 600), m, 7)])
+    y64 = ref.linear_f64(x[rows], w, b, act)
+    absprod = np.abs(x[rows].astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+    check_bound(y1[rows], y64, gemm_bound(y64, absprod, k, "bfloat16", act), "split tail %s" % (case,))
+    if act is None:
+        rs64 = x.astype(np.float64) @ w.astype(np.float64).sum(axis=0)
+        if bias:
+            rs64 = rs64 + b.astype(np.float64).sum()
+        full = np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).sum(axis=0)
+        eps = 2 * (k * 2.0 ** -23 + 2.0 ** -8)
+        assert np.all(np.abs(y1.astype(np.float64).sum(axis=1) - rs64) <= eps * (full + n) + 1e-6)
+
+
 def test_k_zero_writes_epilogue_of_zero():
     x = np.zeros((5, 0), np.float32)
     w = np.zeros((7, 0), np.float32)
