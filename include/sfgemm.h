@@ -88,7 +88,10 @@ int sf_version(void);
  * cuda_gelu_f32 (_cuda_kernels.cu:384,428) and cuda_muls_f32
  * (_cuda_kernels.cu:237-277), which it fuses into the epilogue.
  *
- *   op(A) is M x K: A is stored M x K (lda >= K) when transA == 0.
+ *   op(A) is M x K: A is stored M x K (lda >= K) when transA == 0, or
+ *                   K x M (lda >= M) when transA != 0 ("TN", dW = dY^T X,
+ *                   the four transpose cases of cuda_sgemm
+ *                   _cuda_kernels.cu:1184-1217).
  *   op(B) is K x N: B is stored K x N (ldb >= N) when transB == 0, or
  *                   N x K (ldb >= K) when transB != 0 ("NT", x . W^T).
  *   C is M x N, ldc >= N.
@@ -102,7 +105,6 @@ int sf_version(void);
  * dtype ab_dtype.  F32 inputs run on fp32 MFMA (v_mfma_f32_16x16x4_f32);
  * F16/BF16 inputs on 16-bit MFMA with fp32 accumulation.
  *
- * transA != 0 returns SF_ERR_UNSUPPORTED (no caller on the path uses it).
  * M, N or batch == 0 is a no-op; K == 0 writes epi(0 (+ bias)).
  * The call is asynchronous on `stream`. */
 int sf_gemm(int transA, int transB,
@@ -124,6 +126,18 @@ int sf_gemm_plan(int transA, int transB,
                  void* C, int64_t ldc, int64_t strideC,
                  sf_dtype ab_dtype, sf_dtype c_dtype, float alpha,
                  const void* bias, sf_epilogue epi, char* buf, int len);
+
+/* Sum over one axis: x viewed as [outer, dim_size, inner] (C-contiguous),
+ *   out[o * inner + i] = sum_{d < dim_size} x[(o * dim_size + d) * inner + i].
+ * Replaces cuda_sum_dim_f32 (_cuda_kernels.cu:858-883, decl
+ * _cuda_ops_decl.h:95-96); the bias gradient of a linear layer is the
+ * column sum outer = 1, dim_size = rows, inner = out_features (reference
+ * autograd.py:819).  in_dtype in {F32, F16, BF16}; out_dtype is in_dtype or
+ * F32; fp32 accumulation in an order fixed by the shape (results do not
+ * vary between calls).  dim_size == 0 writes zeros.  Column sums over many
+ * rows use the library's per-device workspace.  Asynchronous on `stream`. */
+int sf_sum_dim(const void* x, void* out, int64_t outer, int64_t dim_size, int64_t inner,
+               sf_dtype in_dtype, sf_dtype out_dtype, void* stream);
 
 /* Fused attention forward, head size D = 64:
  *   O[b] = softmax(scale * Q[b] K[b]^T) V[b],   b in [0, batch),

@@ -15,6 +15,11 @@ so the restatement below is the same sequence of NumPy calls:
   softmax       e = exp(x - max); e / sum(e)          reference nn/functional.py:137-141
   sdpa          scores = q @ k^T; *= scale; softmax; @ v
                                                       reference nn/functional.py:323-357
+  matmul_tn     np.matmul(a^T, b)                     reference autograd.py:296,813-818,
+                                                      _mps_ops.pyx:279-298 (A^T @ B)
+  linear_backward  g @ W, g_2d^T @ x_2d, sum(g_2d, 0) reference autograd.py:793-822
+  sum_dim       np.sum(x, axis=dim)                   reference autograd.py:819;
+                                                      shapes as _cuda_ops.pyx:1710-1741
 
 The *_f64 functions are the closed forms in float64 on the (already
 quantized) inputs: the accuracy oracle for every dtype.
@@ -84,6 +89,32 @@ def sdpa(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float | None = None
     return np.matmul(scores, v)
 
 
+def matmul_tn(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """A^T @ B with A (..., K, M), B (..., K, N): reference autograd.py:296
+    (np.matmul(a_T, g)) and :818 (np.matmul(g_2d.T, x_2d)); the macOS
+    blas_sgemm_tn (_mps_ops.pyx:279-298) computes the same product."""
+    return np.matmul(np.swapaxes(a, -2, -1), b)
+
+
+def linear_backward(g: np.ndarray, x: np.ndarray, w: np.ndarray, has_bias: bool = True):
+    """reference autograd.py:793-822, LinearBackward.backward, the NumPy
+    branch (:816-821): grad_input = g @ W, grad_weight = g_2d.T @ x_2d,
+    grad_bias = np.sum(g_2d, axis=0)."""
+    g_2d = g.reshape(-1, g.shape[-1])
+    x_2d = x.reshape(-1, x.shape[-1])
+    grad_input = np.matmul(g, w)
+    grad_weight = np.matmul(g_2d.T, x_2d)
+    if has_bias:
+        return grad_input, grad_weight, np.sum(g_2d, axis=0)
+    return grad_input, grad_weight
+
+
+def sum_dim(x: np.ndarray, dim: int = -1, keepdim: bool = False) -> np.ndarray:
+    """np.sum over one axis (reference autograd.py:819); output shape as
+    the reference's dev_sum_dim (_cuda_ops.pyx:1710-1741)."""
+    return np.sum(x, axis=dim, keepdims=keepdim)
+
+
 # ------------------------------------------------------- fp64 closed forms
 
 def act_f64(y: np.ndarray, act: str | None) -> np.ndarray:
@@ -106,6 +137,14 @@ def linear_f64(x, w, b=None, act: str | None = None, alpha: float = 1.0) -> np.n
 
 def matmul_f64(a, b) -> np.ndarray:
     return np.matmul(np.asarray(a, np.float64), np.asarray(b, np.float64))
+
+
+def linear_backward_f64(g, x, w):
+    """(g @ W, g_2d^T @ x_2d, column sums of g_2d) in float64."""
+    g64 = np.asarray(g, np.float64)
+    g_2d = g64.reshape(-1, g64.shape[-1])
+    x_2d = np.asarray(x, np.float64).reshape(-1, np.shape(x)[-1])
+    return g64 @ np.asarray(w, np.float64), g_2d.T @ x_2d, g_2d.sum(axis=0)
 
 
 def softmax_f64(x, scale: float = 1.0) -> np.ndarray:

@@ -78,6 +78,8 @@ cdef extern from "sfgemm.h" nogil:
     int sf_gelu(const void* x, void* y, int64_t n, sf_dtype dt, void* stream)
     int sf_muls(const void* x, float s, void* y, int64_t n, sf_dtype dt, void* stream)
     int sf_bias_add_rows(void* C, const void* bias, int64_t M, int64_t N, sf_dtype dt, void* stream)
+    int sf_sum_dim(const void* x, void* out, int64_t outer, int64_t dim_size, int64_t inner,
+                   sf_dtype in_dtype, sf_dtype out_dtype, void* stream)
     int sf_cast(const void* x, sf_dtype in_dtype, void* y, sf_dtype out_dtype, int64_t n, void* stream)
 
     int sf_get_device_count(int* count)
@@ -573,6 +575,25 @@ cdef object _gemm(int transB, int64_t M, int64_t N, int64_t K, int64_t batch,
     return out
 
 
+cdef object _gemm_tn(int64_t M, int64_t N, int64_t K, int64_t batch, a, int64_t strideA, b,
+                     int64_t strideB, tuple out_shape, float alpha):
+    """C = alpha * A^T . B with A stored K x M and B stored K x N."""
+    dt = a.dtype
+    cdef sf_dtype sdt = _sf_dtype(dt)
+    out = _alloc_like(out_shape, dt, a.device_id)
+    cdef void* pa = _ptr(a)
+    cdef void* pb = _ptr(b)
+    cdef void* pc = _ptr(out)
+    cdef int ret
+    cdef int64_t lda = M if M > 0 else 1
+    cdef int64_t ldb = N if N > 0 else 1
+    with nogil:
+        ret = sf_gemm(1, 0, M, N, K, batch, pa, lda, strideA, pb, ldb, strideB,
+                      pc, N, M * N, sdt, sdt, alpha, NULL, SF_EPI_NONE, NULL)
+    _check_kernel(ret)
+    return out
+
+
 def gemm_plan(int transB, int64_t M, int64_t N, int64_t K, int64_t batch,
               uintptr_t ptr_a, int64_t lda, int64_t stride_a,
               uintptr_t ptr_b, int64_t ldb, int64_t stride_b,
@@ -661,6 +682,103 @@ def dev_batched_matmul_nt(gt_a, gt_b, float alpha=1.0):
         raise ValueError("dev_batched_matmul_nt: shapes %s and %s not aligned" % (a_shape, b_shape))
     batch, sa, sb, bshape = _batch_layout(a_shape, b_shape, M * K, N * K, 'dev_batched_matmul_nt')
     return _gemm(1, M, N, K, batch, gt_a, sa, gt_b, K, sb, bshape + (M, N), alpha, None, SF_EPI_NONE)
+
+
+def dev_matmul_tn(gt_a, gt_b, float alpha=1.0):
+    """C = alpha * A^T @ B, A (K,M), B (K,N) -> (M,N): the product of
+    blas_sgemm_tn (reference _mps_ops.pyx:279-298), one launch, no
+    transposed copy of A."""
+    _same_dtype(gt_a, gt_b, 'dev_matmul_tn')
+    if len(gt_a.shape) != 2 or len(gt_b.shape) != 2:
+        raise ValueError("dev_matmul_tn expects 2-D operands")
+    cdef int64_t K = gt_a.shape[0], M = gt_a.shape[1], N = gt_b.shape[1]
+    if gt_b.shape[0] != K:
+        raise ValueError("dev_matmul_tn: shapes %s and %s not aligned" % (gt_a.shape, gt_b.shape))
+    return _gemm_tn(M, N, K, 1, gt_a, 0, gt_b, 0, (M, N), alpha)
+
+
+def dev_batched_matmul_tn(gt_a, gt_b, float alpha=1.0):
+    """C[...] = alpha * A[...]^T @ B[...], A (...,K,M), B (...,K,N): the
+    second-operand gradient of a batched matmul (reference autograd.py:296,
+    np.matmul(a_T, g)), one strided-batched launch."""
+    _same_dtype(gt_a, gt_b, 'dev_batched_matmul_tn')
+    a_shape, b_shape = gt_a.shape, gt_b.shape
+    if len(a_shape) < 2 or len(b_shape) < 2:
+        raise ValueError("dev_batched_matmul_tn expects operands of rank >= 2")
+    cdef int64_t K = a_shape[-2], M = a_shape[-1], N = b_shape[-1]
+    if b_shape[-2] != K:
+        raise ValueError("dev_batched_matmul_tn: shapes %s and %s not aligned" % (a_shape, b_shape))
+    batch, sa, sb, bshape = _batch_layout(a_shape, b_shape, K * M, K * N, 'dev_batched_matmul_tn')
+    return _gemm_tn(M, N, K, batch, gt_a, sa, gt_b, sb, bshape + (M, N), alpha)
+
+
+def dev_sum_dim(gt, int dim=-1, bint keepdim=False):
+    """Sum along dim on the device (reference :1710-1741), fp32
+    accumulation, result in the input dtype."""
+    shape = gt.shape
+    cdef int ndim = len(shape)
+    if ndim == 0:
+        raise ValueError("dev_sum_dim: 0-d tensor")
+    if dim < 0:
+        dim += ndim
+    if dim < 0 or dim >= ndim:
+        raise ValueError("dev_sum_dim: dim out of range for shape %s" % (shape,))
+    cdef int64_t outer = 1, inner = 1
+    for i in range(dim):
+        outer *= shape[i]
+    cdef int64_t dim_size = shape[dim]
+    for i in range(dim + 1, ndim):
+        inner *= shape[i]
+    out_shape = list(shape)
+    if keepdim:
+        out_shape[dim] = 1
+    else:
+        out_shape.pop(dim)
+    if len(out_shape) == 0:
+        out_shape = [1]
+    out = _alloc_like(tuple(out_shape), gt.dtype, gt.device_id)
+    cdef sf_dtype sdt = _sf_dtype(gt.dtype)
+    cdef void* px = _ptr(gt)
+    cdef void* po = _ptr(out)
+    cdef int ret
+    with nogil:
+        ret = sf_sum_dim(px, po, outer, dim_size, inner, sdt, sdt, NULL)
+    _check_kernel(ret)
+    return out
+
+
+def dev_linear_backward(gt_grad, gt_x, gt_weight, bint has_bias=True):
+    """Gradients of y = x @ W^T (+ b) (reference autograd.py:793-822,
+    LinearBackward.backward): grad_input = g @ W (one NN GEMM),
+    grad_weight = g_2d^T @ x_2d (one TN GEMM, no transposed copy),
+    grad_bias = g_2d summed over rows (None without a bias).
+    g (..., N), x (..., K), W (N, K)."""
+    _same_dtype(gt_grad, gt_x, 'dev_linear_backward')
+    _same_dtype(gt_grad, gt_weight, 'dev_linear_backward')
+    if len(gt_weight.shape) != 2 or len(gt_grad.shape) < 1 or len(gt_x.shape) < 1:
+        raise ValueError("dev_linear_backward: g must be (..., N), x (..., K) and W (N, K)")
+    cdef int64_t N = gt_weight.shape[0], K = gt_weight.shape[1]
+    if gt_grad.shape[-1] != N or gt_x.shape[-1] != K or tuple(gt_grad.shape[:-1]) != tuple(gt_x.shape[:-1]):
+        raise ValueError("dev_linear_backward: g %s, x %s and W %s not aligned"
+                         % (gt_grad.shape, gt_x.shape, gt_weight.shape))
+    cdef int64_t M = 1
+    for s in gt_grad.shape[:-1]:
+        M *= s
+    grad_input = _gemm(0, M, K, N, 1, gt_grad, 0, gt_weight, K, 0, tuple(gt_x.shape), 1.0, None, SF_EPI_NONE)
+    grad_weight = _gemm_tn(N, K, M, 1, gt_grad, 0, gt_x, 0, (N, K), 1.0)
+    grad_bias = None
+    cdef sf_dtype sdt = _sf_dtype(gt_grad.dtype)
+    cdef void* pg
+    cdef void* pb
+    cdef int ret
+    if has_bias:
+        grad_bias = _alloc_like((N,), gt_grad.dtype, gt_grad.device_id)
+        pg = _ptr(gt_grad)
+        pb = _ptr(grad_bias)
+        with nogil:
+            ret = sf_sum_dim(pg, pb, 1, M, N, sdt, sdt, NULL)
+        _check_kernel(ret)
+    return grad_input, grad_weight, grad_bias
 
 
 _ACTS = {None: 0, 'none': 0, 'silu': 1, 'gelu': 2, 'gelu_tanh': 2}

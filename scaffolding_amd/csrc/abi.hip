@@ -65,7 +65,7 @@ void tile_dims(int cfg, bool fp32, int& bm, int& bn) {
   (void)fp32;
 }
 
-int launch_gemm16(sf_dtype in, sf_dtype out, bool b_kmajor, int cfg, const GemmParams& p,
+int launch_gemm16(sf_dtype in, sf_dtype out, bool a_kmajor, bool b_kmajor, int cfg, const GemmParams& p,
                   int64_t batch, hipStream_t st) {
   unsigned gx;
   if (cfg == TILE_SKINNY)
@@ -82,8 +82,8 @@ int launch_gemm16(sf_dtype in, sf_dtype out, bool b_kmajor, int cfg, const GemmP
     q.B = static_cast<const uint16_t*>(p.B) + b0 * p.sB;
     q.C = static_cast<uint8_t*>(p.C) + b0 * p.sC * (out == SF_F32 ? 4 : 2);
     const int rc = (in == SF_BF16)
-                       ? launch_gemm16_bf16(out, b_kmajor, cfg, q, gx, static_cast<unsigned>(nb), st)
-                       : launch_gemm16_f16(out, b_kmajor, cfg, q, gx, static_cast<unsigned>(nb), st);
+                       ? launch_gemm16_bf16(out, a_kmajor, b_kmajor, cfg, q, gx, static_cast<unsigned>(nb), st)
+                       : launch_gemm16_f16(out, a_kmajor, b_kmajor, cfg, q, gx, static_cast<unsigned>(nb), st);
     if (rc != SF_OK) return rc;
   }
   return SF_OK;
@@ -111,15 +111,16 @@ static int cu_count_current() {
 static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Picks the 16-bit tile config.  Largest tile that still gives every CU at
-// least one tile; narrow-N problems (P.V, N <= 64) use the 256x64 tile.
-static int choose_tile16(int64_t M, int64_t N, int64_t K, int64_t batch, bool vec, bool b_kmajor,
-                         bool f32_out, int cus) {
+// least one tile; narrow-N problems (P.V, N <= 64) use the 256x64 tile.  An
+// A stored K x M (transA) takes the register-staged tiles only.
+static int choose_tile16(int64_t M, int64_t N, int64_t K, int64_t batch, bool vec, bool a_kmajor,
+                         bool b_kmajor, bool f32_out, int cus) {
   if (!vec) return TILE_GENERIC;
-  if (b_kmajor && M <= 16)
+  if (a_kmajor && b_kmajor && M <= 16)
     return (K == 2048 || K == 4096 || K == 8192) ? TILE_SKINNY_LINE : TILE_SKINNY;
   if (f32_out) return TILE_128x128;
   auto tiles = [&](int64_t bm, int64_t bn) { return cdiv(M, bm) * cdiv(N, bn) * batch; };
-  if (b_kmajor && (K == 64 || (K >= 128 && K % 128 == 0)) && N > 64 && tiles(256, 256) >= cus)
+  if (a_kmajor && b_kmajor && (K == 64 || (K >= 128 && K % 128 == 0)) && N > 64 && tiles(256, 256) >= cus)
     return TILE_NT_BIG;
   if (N <= 64) return tiles(256, 64) >= cus ? TILE_256x64 : TILE_64x64;
   if (tiles(256, 256) >= cus) return TILE_256x256;
@@ -238,6 +239,7 @@ struct GemmPlan {
   GemmParams p;
   int cfg;
   bool fp32;
+  bool a_kmajor;
   bool b_kmajor;
   bool noop;
 };
@@ -253,7 +255,6 @@ static int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K,
     return fail(SF_ERR_INVALID_ARG, "sf_gemm: unknown dtype (%d, %d)", (int)ab_dtype, (int)c_dtype);
   if ((int)epi < SF_EPI_NONE || (int)epi > SF_EPI_GELU_TANH)
     return fail(SF_ERR_INVALID_ARG, "sf_gemm: unknown epilogue %d", (int)epi);
-  if (transA) return fail(SF_ERR_UNSUPPORTED, "sf_gemm: transA is not supported");
   if (c_dtype != ab_dtype && c_dtype != SF_F32)
     return fail(SF_ERR_UNSUPPORTED, "sf_gemm: output dtype must equal the input dtype or be F32");
   if (M < 0 || N < 0 || K < 0 || batch < 0)
@@ -270,15 +271,18 @@ static int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K,
     plan.noop = true;
     return SF_OK;
   }
+  // op(A) = A (M x K, K-contiguous) or, with transA, the transpose of A
+  // stored K x M; op(B) likewise with transB for B stored N x K.
+  const bool a_kmajor = transA == 0;
   const bool b_kmajor = transB != 0;
   if ((need_c && C == nullptr) || (K > 0 && (A == nullptr || B == nullptr)))
     return fail(SF_ERR_INVALID_ARG, "sf_gemm: null operand pointer");
-  if (lda < (K > 0 ? K : 1) || ldb < (b_kmajor ? (K > 0 ? K : 1) : N) || ldc < N)
+  if (lda < (a_kmajor ? (K > 0 ? K : 1) : M) || ldb < (b_kmajor ? (K > 0 ? K : 1) : N) || ldc < N)
     return fail(SF_ERR_INVALID_ARG,
                 "sf_gemm: leading dimension too small (lda=%lld ldb=%lld ldc=%lld for M=%lld "
-                "N=%lld K=%lld transB=%d)",
+                "N=%lld K=%lld transA=%d transB=%d)",
                 (long long)lda, (long long)ldb, (long long)ldc, (long long)M, (long long)N,
-                (long long)K, transB);
+                (long long)K, transA, transB);
   if (strideA < 0 || strideB < 0 || strideC < 0)
     return fail(SF_ERR_INVALID_ARG, "sf_gemm: negative batch stride");
   if (batch > 1 && strideC < (M - 1) * ldc + N)
@@ -292,21 +296,22 @@ static int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K,
   p.M = (int)M; p.N = (int)N; p.K = (int)K;
   p.alpha = alpha;
   p.epi = (int)epi;
+  plan.a_kmajor = a_kmajor;
   plan.b_kmajor = b_kmajor;
   const int cus = cu_count_current();
   int bm, bn;
   if (ab_dtype == SF_F32) {
     const bool vec = al16(A) && al16(B) && (lda % 4 == 0) && (ldb % 4 == 0) &&
                      (strideA % 4 == 0) && (strideB % 4 == 0) && (K % 4 == 0) &&
-                     (b_kmajor || N % 4 == 0);
+                     (a_kmajor || M % 4 == 0) && (b_kmajor || N % 4 == 0);
     plan.fp32 = true;
     plan.cfg = choose_tile32(M, N, batch, vec, cus);
   } else {
     const bool vec = al16(A) && al16(B) && (lda % 8 == 0) && (ldb % 8 == 0) &&
                      (strideA % 8 == 0) && (strideB % 8 == 0) && (K % 8 == 0) &&
-                     (b_kmajor || N % 8 == 0);
+                     (a_kmajor || M % 8 == 0) && (b_kmajor || N % 8 == 0);
     plan.fp32 = false;
-    plan.cfg = choose_tile16(M, N, K, batch, vec, b_kmajor, c_dtype == SF_F32, cus);
+    plan.cfg = choose_tile16(M, N, K, batch, vec, a_kmajor, b_kmajor, c_dtype == SF_F32, cus);
     // The LDS-DMA kernel addresses each operand with 32-bit byte offsets.
     if (plan.cfg == TILE_NT_BIG && (M * lda * 2 >= (int64_t(1) << 31) || N * ldb * 2 >= (int64_t(1) << 31)))
       plan.cfg = TILE_256x256;
@@ -359,17 +364,17 @@ int sf_gemm(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t bat
                         strideC, ab_dtype, c_dtype, alpha, bias, epi, true, plan);
   if (rc != SF_OK || plan.noop) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (plan.fp32) return launch_gemm32(plan.b_kmajor, plan.cfg, plan.p, batch, st);
+  if (plan.fp32) return launch_gemm32(plan.a_kmajor, plan.b_kmajor, plan.cfg, plan.p, batch, st);
   if (plan.p.split > 0) {
     const int nsplit = plan.p.tiles_m * plan.p.tiles_n - plan.p.full_tiles;
     rc = split_workspace_acquire((size_t)nsplit * plan.p.split * (256u * 256u * 4u), nsplit, st, &plan.p.ws,
                                  &plan.p.counters);
     if (rc != SF_OK) return rc;
-    rc = launch_gemm16(ab_dtype, c_dtype, plan.b_kmajor, plan.cfg, plan.p, batch, st);
+    rc = launch_gemm16(ab_dtype, c_dtype, plan.a_kmajor, plan.b_kmajor, plan.cfg, plan.p, batch, st);
     const int rc2 = split_workspace_release(st);
     return rc != SF_OK ? rc : rc2;
   }
-  return launch_gemm16(ab_dtype, c_dtype, plan.b_kmajor, plan.cfg, plan.p, batch, st);
+  return launch_gemm16(ab_dtype, c_dtype, plan.a_kmajor, plan.b_kmajor, plan.cfg, plan.p, batch, st);
 }
 
 int sf_gemm_plan(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t batch,
@@ -420,6 +425,31 @@ int sf_attention(const void* Q, int64_t ldq, int64_t strideQ, const void* K, int
     return fail(SF_ERR_UNSUPPORTED, "sf_attention: rows must be 16-byte aligned");
   return launch_attention(Q, K, V, O, batch, Sq, Sk, strideQ, strideK, strideV, strideO, ldq, ldk, ldv, ldo,
                           scale, dtype, static_cast<hipStream_t>(stream));
+}
+
+int sf_sum_dim(const void* x, void* out, int64_t outer, int64_t dim_size, int64_t inner, sf_dtype in_dtype,
+               sf_dtype out_dtype, void* stream) {
+  g_err[0] = 0;
+  if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype))
+    return fail(SF_ERR_INVALID_ARG, "sf_sum_dim: unknown dtype");
+  if (out_dtype != in_dtype && out_dtype != SF_F32)
+    return fail(SF_ERR_UNSUPPORTED, "sf_sum_dim: output dtype must equal the input dtype or be F32");
+  if (outer < 0 || dim_size < 0 || inner < 0) return fail(SF_ERR_INVALID_ARG, "sf_sum_dim: negative size");
+  if (inner > INT32_MAX || dim_size > INT32_MAX || outer > INT32_MAX)
+    return fail(SF_ERR_UNSUPPORTED, "sf_sum_dim: outer, dim_size and inner must be < 2^31");
+  if (outer == 0 || inner == 0) return SF_OK;
+  if (x == nullptr || out == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_sum_dim: null pointer");
+  if (inner > 1 && outer > 65535) return fail(SF_ERR_UNSUPPORTED, "sf_sum_dim: outer must be < 65536 when inner > 1");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int S = sum_dim_parts(outer, dim_size, inner, cu_count_current());
+  if (S == 1) return launch_sum_dim(x, out, outer, dim_size, inner, in_dtype, out_dtype, nullptr, 1, st);
+  float* ws = nullptr;
+  int* cnt = nullptr;
+  int rc = split_workspace_acquire((size_t)S * (size_t)outer * (size_t)inner * sizeof(float), 0, st, &ws, &cnt);
+  if (rc != SF_OK) return rc;
+  rc = launch_sum_dim(x, out, outer, dim_size, inner, in_dtype, out_dtype, ws, S, st);
+  const int rc2 = split_workspace_release(st);
+  return rc != SF_OK ? rc : rc2;
 }
 
 int sf_softmax_rows(const void* x, void* y, int64_t rows, int64_t cols, sf_dtype in_dtype,

@@ -3,8 +3,10 @@
 //
 //   C[b] = epi(alpha * A[b] . op(B[b]) (+ bias))      row-major
 //
-// A is M x K (K-contiguous).  B is either N x K (K-contiguous, "NT":
-// x . W^T, QK^T) or K x N (N-contiguous, "NN": A . B, P . V).
+// A is M x K (K-contiguous) or, with A_KMAJOR = false, stored K x M
+// (M-contiguous: the product uses its transpose, "TN" / "TT": dW = dY^T X).
+// B is either N x K (K-contiguous, "NT": x . W^T, QK^T) or K x N
+// (N-contiguous, "NN": A . B, P . V).
 //
 // Work decomposition
 //   * one workgroup per BM x BN output tile, grid.y = batch;
@@ -28,10 +30,11 @@
 // c ^ (r & 7).  An MFMA operand read (16 lanes on 16 consecutive rows, same
 // chunk) therefore touches 8 distinct slots per 8 lanes — no bank conflicts
 // for ds_read_b128 — and the 16-byte global->LDS stores of a row are a
-// permutation of the row's slots.  An N-contiguous B tile is transposed on
-// its way into LDS (each 16-byte global load of 8 consecutive n scatters
-// into 8 rows); the lane->k assignment makes each ds_write_b16 instruction
-// cover 64 distinct 2-byte slots of one 128-byte row group.
+// permutation of the row's slots.  An N-contiguous B tile (and an
+// M-contiguous A tile) is transposed on its way into LDS (each 16-byte
+// global load of 8 consecutive n scatters into 8 rows); the lane->k
+// assignment makes each ds_write_b16 instruction cover 64 distinct 2-byte
+// slots of one 128-byte row group.
 #pragma once
 
 #include "sf_common.hpp"
@@ -118,7 +121,7 @@ __device__ __forceinline__ void load_bias4(const void* bias, int n, int N, float
 }
 
 template <typename TIn, typename TOut, int BM, int BN, int WAVES_M, int WAVES_N, bool B_KMAJOR,
-          bool VEC>
+          bool VEC, bool A_KMAJOR = true>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmParams p) {
   constexpr int NT = WAVES_M * WAVES_N * 64;
   constexpr int BK = 64;
@@ -168,26 +171,48 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmParam
 
   // ---- global -> registers ------------------------------------------------
   auto load_tiles = [&](int k0) {
+    if constexpr (!A_KMAJOR) {
+      // A is K x M: thread -> (k = idx % BK, 8-wide m chunk = idx / BK).
 #pragma unroll
-    for (int i = 0; i < A_LD; ++i) {
-      int idx = tid + i * NT;
-      int row = idx / CH, ch = idx % CH;
-      int gm = m0 + row, gk = k0 + ch * 8;
-      if constexpr (VEC) {
-        const u32x4* pa = reinterpret_cast<const u32x4*>(A + (int64_t)gm * lda + gk);
-        // The 256 x 64 tile serves N <= 64 (one tile column): every A row
-        // panel is read exactly once, so it streams past the caches.
-        if constexpr (BM == 256 && BN == 64)
-          ra[i] = (gm < M && gk < K) ? __builtin_nontemporal_load(pa) : u32x4{0u, 0u, 0u, 0u};
-        else
-          ra[i] = (gm < M && gk < K) ? *pa : u32x4{0u, 0u, 0u, 0u};
-      } else {
-        uint16_t e[8];
+      for (int i = 0; i < A_LD; ++i) {
+        int idx = tid + i * NT;
+        int k = idx % BK, mc = idx / BK;
+        int gk = k0 + k, gm = m0 + mc * 8;
+        if constexpr (VEC) {
+          ra[i] = (gk < K && gm < M)
+                      ? *reinterpret_cast<const u32x4*>(A + (int64_t)gk * lda + gm)
+                      : u32x4{0u, 0u, 0u, 0u};
+        } else {
+          uint16_t e[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q)
-          e[q] = (gm < M && gk + q < K) ? A[(int64_t)gm * lda + gk + q] : (uint16_t)0;
-        ra[i] = u32x4{e[0] | ((uint32_t)e[1] << 16), e[2] | ((uint32_t)e[3] << 16),
-                      e[4] | ((uint32_t)e[5] << 16), e[6] | ((uint32_t)e[7] << 16)};
+          for (int q = 0; q < 8; ++q)
+            e[q] = (gk < K && gm + q < M) ? A[(int64_t)gk * lda + gm + q] : (uint16_t)0;
+          ra[i] = u32x4{e[0] | ((uint32_t)e[1] << 16), e[2] | ((uint32_t)e[3] << 16),
+                        e[4] | ((uint32_t)e[5] << 16), e[6] | ((uint32_t)e[7] << 16)};
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < A_LD; ++i) {
+        int idx = tid + i * NT;
+        int row = idx / CH, ch = idx % CH;
+        int gm = m0 + row, gk = k0 + ch * 8;
+        if constexpr (VEC) {
+          const u32x4* pa = reinterpret_cast<const u32x4*>(A + (int64_t)gm * lda + gk);
+          // The 256 x 64 tile serves N <= 64 (one tile column): every A row
+          // panel is read exactly once, so it streams past the caches.
+          if constexpr (BM == 256 && BN == 64)
+            ra[i] = (gm < M && gk < K) ? __builtin_nontemporal_load(pa) : u32x4{0u, 0u, 0u, 0u};
+          else
+            ra[i] = (gm < M && gk < K) ? *pa : u32x4{0u, 0u, 0u, 0u};
+        } else {
+          uint16_t e[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q)
+            e[q] = (gm < M && gk + q < K) ? A[(int64_t)gm * lda + gk + q] : (uint16_t)0;
+          ra[i] = u32x4{e[0] | ((uint32_t)e[1] << 16), e[2] | ((uint32_t)e[3] << 16),
+                        e[4] | ((uint32_t)e[5] << 16), e[6] | ((uint32_t)e[7] << 16)};
+        }
       }
     }
     if constexpr (B_KMAJOR) {
@@ -236,11 +261,26 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmParam
   auto store_tiles = [&](int stage) {
     uint8_t* As = smem + stage * STAGE;
     uint8_t* Bs = As + A_BYTES;
+    if constexpr (A_KMAJOR) {
 #pragma unroll
-    for (int i = 0; i < A_LD; ++i) {
-      int idx = tid + i * NT;
-      int row = idx / CH, ch = idx % CH;
-      *reinterpret_cast<u32x4*>(As + swz(row, ch)) = ra[i];
+      for (int i = 0; i < A_LD; ++i) {
+        int idx = tid + i * NT;
+        int row = idx / CH, ch = idx % CH;
+        *reinterpret_cast<u32x4*>(As + swz(row, ch)) = ra[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < A_LD; ++i) {
+        int idx = tid + i * NT;
+        int k = idx % BK, mc = idx / BK;
+        uint32_t w[4] = {ra[i][0], ra[i][1], ra[i][2], ra[i][3]};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          int m = mc * 8 + e;
+          uint16_t v = static_cast<uint16_t>(w[e >> 1] >> ((e & 1) * 16));
+          *reinterpret_cast<uint16_t*>(As + swz(m, k >> 3) + ((k & 7) << 1)) = v;
+        }
+      }
     }
     if constexpr (B_KMAJOR) {
 #pragma unroll

@@ -3,9 +3,9 @@
 
 namespace sf {
 
-int launch_gemm16_f16(sf_dtype out, bool b_kmajor, int cfg, const GemmParams& p, unsigned gx,
+int launch_gemm16_f16(sf_dtype out, bool a_kmajor, bool b_kmajor, int cfg, const GemmParams& p, unsigned gx,
                       unsigned gy, hipStream_t st) {
-  return launch16_in<F16>(SF_F16, out, b_kmajor, cfg, p, gx, gy, st);
+  return launch16_in<F16>(SF_F16, out, a_kmajor, b_kmajor, cfg, p, gx, gy, st);
 }
 
 }  // namespace sf

@@ -25,51 +25,53 @@ static int launch_skinny_line(const GemmParams& p, const dim3& g, hipStream_t st
   return fail(SF_ERR_INVALID_ARG, "skinny line kernel: K=%d is not 2048, 4096 or 8192", p.K);
 }
 
-template <typename TIn, typename TOut, bool KM>
+// KM: B K-contiguous; AKM: A K-contiguous (false: A stored K x M).  The
+// LDS-DMA, skinny and row-segment kernels need both K-contiguous.
+template <typename TIn, typename TOut, bool KM, bool AKM>
 static int launch16_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hipStream_t st) {
   const dim3 g(gx, gy);
   switch (cfg) {
     case TILE_256x256:
-      hipLaunchKernelGGL((gemm16_kernel<TIn, TOut, 256, 256, 2, 4, KM, true>), g, dim3(512), 0, st, p);
+      hipLaunchKernelGGL((gemm16_kernel<TIn, TOut, 256, 256, 2, 4, KM, true, AKM>), g, dim3(512), 0, st, p);
       break;
     case TILE_256x128:
-      hipLaunchKernelGGL((gemm16_kernel<TIn, TOut, 256, 128, 4, 2, KM, true>), g, dim3(512), 0, st, p);
+      hipLaunchKernelGGL((gemm16_kernel<TIn, TOut, 256, 128, 4, 2, KM, true, AKM>), g, dim3(512), 0, st, p);
       break;
     case TILE_128x128:
-      hipLaunchKernelGGL((gemm16_kernel<TIn, TOut, 128, 128, 2, 2, KM, true>), g, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((gemm16_kernel<TIn, TOut, 128, 128, 2, 2, KM, true, AKM>), g, dim3(256), 0, st, p);
       break;
     case TILE_256x64:
-      hipLaunchKernelGGL((gemm16_kernel<TIn, TOut, 256, 64, 4, 1, KM, true>), g, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((gemm16_kernel<TIn, TOut, 256, 64, 4, 1, KM, true, AKM>), g, dim3(256), 0, st, p);
       break;
     case TILE_64x64:
-      hipLaunchKernelGGL((gemm16_kernel<TIn, TOut, 64, 64, 2, 2, KM, true>), g, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((gemm16_kernel<TIn, TOut, 64, 64, 2, 2, KM, true, AKM>), g, dim3(256), 0, st, p);
       break;
     case TILE_GENERIC:
-      hipLaunchKernelGGL((gemm16_kernel<TIn, TOut, 64, 64, 2, 2, KM, false>), g, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((gemm16_kernel<TIn, TOut, 64, 64, 2, 2, KM, false, AKM>), g, dim3(256), 0, st, p);
       break;
     case TILE_NT_BIG:
-      if constexpr (KM) {
+      if constexpr (KM && AKM) {
         if (p.K == 64)
           hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut, 1>), g, dim3(512), 0, st, p);
         else
           hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut, 2>), g, dim3(512), 0, st, p);
         break;
       }
-      return fail(SF_ERR_UNSUPPORTED, "the 256x256 NT kernel needs a K-contiguous B");
+      return fail(SF_ERR_UNSUPPORTED, "the 256x256 NT kernel needs K-contiguous A and B");
     case TILE_SKINNY:
-      if constexpr (KM) {
+      if constexpr (KM && AKM) {
         // grid.x = ceil(N / 32): 2 row blocks per workgroup, K split over 4 waves.
         hipLaunchKernelGGL((skinny16_kernel<TIn, TOut, 4, 2, 8>), g, dim3(256), 0, st, p);
         break;
       }
-      return fail(SF_ERR_UNSUPPORTED, "skinny kernel needs a K-contiguous B");
+      return fail(SF_ERR_UNSUPPORTED, "skinny kernels need K-contiguous A and B");
     case TILE_SKINNY_LINE:
-      if constexpr (KM) {
+      if constexpr (KM && AKM) {
         const int rc = launch_skinny_line<TIn, TOut>(p, g, st);
         if (rc != SF_OK) return rc;
         break;
       }
-      return fail(SF_ERR_UNSUPPORTED, "skinny kernel needs a K-contiguous B");
+      return fail(SF_ERR_UNSUPPORTED, "skinny kernels need K-contiguous A and B");
     default:
       return fail(SF_ERR_INVALID_ARG, "unknown tile config %d", cfg);
   }
@@ -77,29 +79,29 @@ static int launch16_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hi
 }
 
 // Only the tiles the dispatcher picks for an fp32 output of 16-bit inputs.
-template <typename TIn, bool KM>
+template <typename TIn, bool KM, bool AKM>
 static int launch16_f32out(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hipStream_t st) {
   const dim3 g(gx, gy);
   switch (cfg) {
     case TILE_128x128:
-      hipLaunchKernelGGL((gemm16_kernel<TIn, float, 128, 128, 2, 2, KM, true>), g, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((gemm16_kernel<TIn, float, 128, 128, 2, 2, KM, true, AKM>), g, dim3(256), 0, st, p);
       break;
     case TILE_GENERIC:
-      hipLaunchKernelGGL((gemm16_kernel<TIn, float, 64, 64, 2, 2, KM, false>), g, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((gemm16_kernel<TIn, float, 64, 64, 2, 2, KM, false, AKM>), g, dim3(256), 0, st, p);
       break;
     case TILE_SKINNY:
-      if constexpr (KM) {
+      if constexpr (KM && AKM) {
         hipLaunchKernelGGL((skinny16_kernel<TIn, float, 4, 2, 8>), g, dim3(256), 0, st, p);
         break;
       }
-      return fail(SF_ERR_UNSUPPORTED, "skinny kernel needs a K-contiguous B");
+      return fail(SF_ERR_UNSUPPORTED, "skinny kernels need K-contiguous A and B");
     case TILE_SKINNY_LINE:
-      if constexpr (KM) {
+      if constexpr (KM && AKM) {
         const int rc = launch_skinny_line<TIn, float>(p, g, st);
         if (rc != SF_OK) return rc;
         break;
       }
-      return fail(SF_ERR_UNSUPPORTED, "skinny kernel needs a K-contiguous B");
+      return fail(SF_ERR_UNSUPPORTED, "skinny kernels need K-contiguous A and B");
     default:
       return fail(SF_ERR_INVALID_ARG, "tile config %d has no fp32-output variant", cfg);
   }
@@ -107,14 +109,21 @@ static int launch16_f32out(int cfg, const GemmParams& p, unsigned gx, unsigned g
 }
 
 template <typename TIn>
-static int launch16_in(sf_dtype in, sf_dtype out, bool b_kmajor, int cfg, const GemmParams& p,
+static int launch16_in(sf_dtype in, sf_dtype out, bool a_kmajor, bool b_kmajor, int cfg, const GemmParams& p,
                        unsigned gx, unsigned gy, hipStream_t st) {
-  if (out == SF_F32)
-    return b_kmajor ? launch16_f32out<TIn, true>(cfg, p, gx, gy, st)
-                    : launch16_f32out<TIn, false>(cfg, p, gx, gy, st);
   (void)in;
-  return b_kmajor ? launch16_t<TIn, TIn, true>(cfg, p, gx, gy, st)
-                  : launch16_t<TIn, TIn, false>(cfg, p, gx, gy, st);
+  if (out == SF_F32) {
+    if (a_kmajor)
+      return b_kmajor ? launch16_f32out<TIn, true, true>(cfg, p, gx, gy, st)
+                      : launch16_f32out<TIn, false, true>(cfg, p, gx, gy, st);
+    return b_kmajor ? launch16_f32out<TIn, true, false>(cfg, p, gx, gy, st)
+                    : launch16_f32out<TIn, false, false>(cfg, p, gx, gy, st);
+  }
+  if (a_kmajor)
+    return b_kmajor ? launch16_t<TIn, TIn, true, true>(cfg, p, gx, gy, st)
+                    : launch16_t<TIn, TIn, false, true>(cfg, p, gx, gy, st);
+  return b_kmajor ? launch16_t<TIn, TIn, true, false>(cfg, p, gx, gy, st)
+                  : launch16_t<TIn, TIn, false, false>(cfg, p, gx, gy, st);
 }
 
 }  // namespace sf

@@ -4,18 +4,18 @@
 
 namespace sf {
 
-template <bool KM>
+template <bool KM, bool AKM>
 static int launch32_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hipStream_t st) {
   const dim3 g(gx, gy);
   switch (cfg) {
     case TILE_128x128:
-      hipLaunchKernelGGL((gemm32_kernel<128, 128, 2, 2, KM, true>), g, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((gemm32_kernel<128, 128, 2, 2, KM, true, AKM>), g, dim3(256), 0, st, p);
       break;
     case TILE_64x64:
-      hipLaunchKernelGGL((gemm32_kernel<64, 64, 2, 2, KM, true>), g, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((gemm32_kernel<64, 64, 2, 2, KM, true, AKM>), g, dim3(256), 0, st, p);
       break;
     case TILE_GENERIC:
-      hipLaunchKernelGGL((gemm32_kernel<64, 64, 2, 2, KM, false>), g, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((gemm32_kernel<64, 64, 2, 2, KM, false, AKM>), g, dim3(256), 0, st, p);
       break;
     default:
       return fail(SF_ERR_INVALID_ARG, "tile config %d has no fp32 variant", cfg);
@@ -23,7 +23,7 @@ static int launch32_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hi
   return check_launch(tile_name(cfg));
 }
 
-int launch_gemm32(bool b_kmajor, int cfg, const GemmParams& p, int64_t batch, hipStream_t st) {
+int launch_gemm32(bool a_kmajor, bool b_kmajor, int cfg, const GemmParams& p, int64_t batch, hipStream_t st) {
   const unsigned gx = static_cast<unsigned>(p.tiles_m) * static_cast<unsigned>(p.tiles_n);
   // grid.y is limited to 65535: walk the batch in chunks.
   for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
@@ -32,8 +32,11 @@ int launch_gemm32(bool b_kmajor, int cfg, const GemmParams& p, int64_t batch, hi
     q.A = static_cast<const float*>(p.A) + b0 * p.sA;
     q.B = static_cast<const float*>(p.B) + b0 * p.sB;
     q.C = static_cast<float*>(p.C) + b0 * p.sC;
-    const int rc = b_kmajor ? launch32_t<true>(cfg, q, gx, static_cast<unsigned>(nb), st)
-                            : launch32_t<false>(cfg, q, gx, static_cast<unsigned>(nb), st);
+    const unsigned gy = static_cast<unsigned>(nb);
+    const int rc = a_kmajor ? (b_kmajor ? launch32_t<true, true>(cfg, q, gx, gy, st)
+                                        : launch32_t<false, true>(cfg, q, gx, gy, st))
+                            : (b_kmajor ? launch32_t<true, false>(cfg, q, gx, gy, st)
+                                        : launch32_t<false, false>(cfg, q, gx, gy, st));
     if (rc != SF_OK) return rc;
   }
   return SF_OK;

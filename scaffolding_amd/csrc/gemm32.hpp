@@ -22,24 +22,27 @@
 //   B, N-major   [BK][BN + 4]   N-contiguous; the X operand is a scalar per
 //                               lane per step (16 consecutive n per group,
 //                               groups 4 rows = 16 banks apart).
+//   A, M-major   [BK][BM + 4]   A stored K x M (the product uses A^T); the
+//                               Y operand is read like the N-major B.
 #pragma once
 
 #include "gemm16.hpp"
 
 namespace sf {
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool B_KMAJOR, bool VEC>
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool B_KMAJOR, bool VEC, bool A_KMAJOR = true>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm32_kernel(GemmParams p) {
   constexpr int NT = WAVES_M * WAVES_N * 64;
   constexpr int BK = 32;
   constexpr int CH = BK / 4;  // float4 chunks per K-contiguous row
   constexpr int AP = BK + 4;  // A / K-major-B row pitch (floats)
   constexpr int BP = BN + 4;  // N-major-B row pitch (floats)
+  constexpr int MP = BM + 4;  // M-major-A row pitch (floats)
   constexpr int WM = BM / WAVES_M;
   constexpr int WN = BN / WAVES_N;
   constexpr int FM = WM / 16;
   constexpr int FN = WN / 16;
-  constexpr int A_FLOATS = BM * AP;
+  constexpr int A_FLOATS = A_KMAJOR ? BM * AP : BK * MP;
   constexpr int B_FLOATS = B_KMAJOR ? BN * AP : BK * BP;
   constexpr int STAGE = A_FLOATS + B_FLOATS;
   static_assert((BM * CH) % NT == 0 && (BN * CH) % NT == 0, "tile loads must divide evenly");
@@ -92,7 +95,12 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm32_kernel(GemmParam
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
       int idx = tid + i * NT;
-      ra[i] = load4(A, lda, m0 + idx / CH, k0 + (idx % CH) * 4, M, K);
+      if constexpr (A_KMAJOR) {
+        ra[i] = load4(A, lda, m0 + idx / CH, k0 + (idx % CH) * 4, M, K);
+      } else {
+        constexpr int MC = BM / 4;
+        ra[i] = load4(A, lda, k0 + idx / MC, m0 + (idx % MC) * 4, K, M);
+      }
     }
 #pragma unroll
     for (int i = 0; i < B_LD; ++i) {
@@ -112,7 +120,12 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm32_kernel(GemmParam
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
       int idx = tid + i * NT;
-      *reinterpret_cast<f32x4*>(As + (idx / CH) * AP + (idx % CH) * 4) = ra[i];
+      if constexpr (A_KMAJOR) {
+        *reinterpret_cast<f32x4*>(As + (idx / CH) * AP + (idx % CH) * 4) = ra[i];
+      } else {
+        constexpr int MC = BM / 4;
+        *reinterpret_cast<f32x4*>(As + (idx / MC) * MP + (idx % MC) * 4) = ra[i];
+      }
     }
 #pragma unroll
     for (int i = 0; i < B_LD; ++i) {
@@ -131,39 +144,37 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm32_kernel(GemmParam
     const float* Bs = As + A_FLOATS;
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
-      f32x4 ya[FM];
+      // K-major tiles: one float4 per fragment covers the four steps.
+      f32x4 ya4[FM], xb4[FN];
+      if constexpr (A_KMAJOR) {
 #pragma unroll
-      for (int j = 0; j < FM; ++j) {
-        int row = wm * WM + j * 16 + (lane & 15);
-        ya[j] = *reinterpret_cast<const f32x4*>(As + row * AP + kk * 16 + 4 * g);
+        for (int j = 0; j < FM; ++j) {
+          int row = wm * WM + j * 16 + (lane & 15);
+          ya4[j] = *reinterpret_cast<const f32x4*>(As + row * AP + kk * 16 + 4 * g);
+        }
       }
       if constexpr (B_KMAJOR) {
-        f32x4 xb[FN];
 #pragma unroll
         for (int i = 0; i < FN; ++i) {
           int row = wn * WN + i * 16 + (lane & 15);
-          xb[i] = *reinterpret_cast<const f32x4*>(Bs + row * AP + kk * 16 + 4 * g);
+          xb4[i] = *reinterpret_cast<const f32x4*>(Bs + row * AP + kk * 16 + 4 * g);
         }
+      }
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+      for (int s = 0; s < 4; ++s) {
+        const int k = kk * 16 + 4 * g + s;
+        float ys[FM], xs[FN];
 #pragma unroll
-          for (int i = 0; i < FN; ++i)
+        for (int j = 0; j < FM; ++j)
+          ys[j] = A_KMAJOR ? ya4[j][s] : As[k * MP + wm * WM + j * 16 + (lane & 15)];
 #pragma unroll
-            for (int j = 0; j < FM; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xb[i][s], ya[j][s], acc[i][j], 0, 0, 0);
-      } else {
+        for (int i = 0; i < FN; ++i)
+          xs[i] = B_KMAJOR ? xb4[i][s] : Bs[k * BP + wn * WN + i * 16 + (lane & 15)];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          float xb[FN];
-          const float* brow = Bs + (kk * 16 + 4 * g + s) * BP + wn * WN + (lane & 15);
+        for (int i = 0; i < FN; ++i)
 #pragma unroll
-          for (int i = 0; i < FN; ++i) xb[i] = brow[i * 16];
-#pragma unroll
-          for (int i = 0; i < FN; ++i)
-#pragma unroll
-            for (int j = 0; j < FM; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xb[i], ya[j][s], acc[i][j], 0, 0, 0);
-        }
+          for (int j = 0; j < FM; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xs[i], ys[j], acc[i][j], 0, 0, 0);
       }
     }
   };

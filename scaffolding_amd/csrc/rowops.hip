@@ -1,6 +1,7 @@
 // rowops.hip — HBM-bound row and elementwise kernels of the path:
 // row softmax (with the SDPA pre-scale folded in), standalone SiLU / GELU /
-// scalar-multiply / bias-add, dtype casts and a zero fill.
+// scalar-multiply / bias-add, the sum over one axis (bias gradients),
+// dtype casts and a zero fill.
 #include "sf_internal.hpp"
 
 namespace sf {
@@ -221,6 +222,106 @@ __global__ __launch_bounds__(256) void zero_kernel(uint8_t* p, size_t nbytes) {
   if (tid < nbytes - tail0) p[tail0 + tid] = 0;
 }
 
+
+// ---------------------------------------------------------------------
+// Sum over the middle axis of x viewed as [outer, D, inner], fp32
+// accumulation:  out[o, i] = sum_{d < D} x[o, d, i].
+//
+// Columns (inner > 1, e.g. a bias gradient: outer 1, D rows, inner
+// columns): each lane owns 8 consecutive columns; the 4 waves of a
+// workgroup take every 4th d of the workgroup's d-range
+// [D s / S, D (s + 1) / S); the waves' sums are added in wave order through
+// LDS.  With S > 1 the workgroup writes its fp32 partial to
+// ws[(o S + s) inner + i] and sum_parts_kernel adds the S partials in
+// order, so the result does not depend on scheduling.
+// Rows (inner == 1): one wave per o, lanes stride over d, then a fixed
+// xor butterfly.
+// ---------------------------------------------------------------------
+template <typename TI, typename TO, bool VEC>
+__global__ __launch_bounds__(256) void sum_cols_kernel(const void* __restrict__ x, void* __restrict__ out,
+                                                       float* __restrict__ ws, int64_t D, int64_t inner,
+                                                       int S) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t o = blockIdx.z;
+  const int s = blockIdx.y;
+  const int64_t i0 = ((int64_t)blockIdx.x * 64 + lane) * 8;
+  const int64_t d0 = D * s / S, d1 = D * (s + 1) / S;
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  if (i0 < inner) {
+    const int64_t base = o * D * inner + i0;
+    for (int64_t d = d0 + wave; d < d1; d += 4) {
+      float v[8];
+      if constexpr (VEC) {
+        Chunk8<TI>::load(x, base + d * inner, v);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (i0 + e < inner) ? Chunk8<TI>::get(x, base + d * inner + e) : 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += v[e];
+    }
+  }
+  __shared__ float red[4][8][64];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) red[wave][e][lane] = acc[e];
+  __syncthreads();
+  if (wave != 0 || i0 >= inner) return;
+  float t[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) t[e] = ((red[0][e][lane] + red[1][e][lane]) + red[2][e][lane]) + red[3][e][lane];
+  if (S == 1) {
+    const int64_t ob = o * inner + i0;
+    if constexpr (VEC) {
+      Chunk8<TO>::store(out, ob, t);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (i0 + e < inner) Chunk8<TO>::put(out, ob + e, t[e]);
+    }
+  } else {
+    float* w = ws + ((int64_t)o * S + s) * inner + i0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (i0 + e < inner) w[e] = t[e];
+  }
+}
+
+template <typename TO>
+__global__ __launch_bounds__(256) void sum_parts_kernel(const float* __restrict__ ws, void* __restrict__ out,
+                                                        int64_t outer, int64_t inner, int S) {
+  const int64_t n = outer * inner;
+  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < n; idx += (int64_t)gridDim.x * 256) {
+    const int64_t o = idx / inner, i = idx - o * inner;
+    const float* w = ws + o * S * inner + i;
+    float t = 0.f;
+    for (int s = 0; s < S; ++s) t += w[(int64_t)s * inner];
+    Chunk8<TO>::put(out, idx, t);
+  }
+}
+
+template <typename TI, typename TO, bool VEC>
+__global__ __launch_bounds__(256) void sum_rows_kernel(const void* __restrict__ x, void* __restrict__ out,
+                                                       int64_t outer, int64_t D) {
+  const int lane = threadIdx.x & 63;
+  const int64_t o = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (o >= outer) return;
+  float acc = 0.f;
+  if constexpr (VEC) {
+    for (int64_t c = (int64_t)lane * 8; c < D; c += 512) {
+      float v[8];
+      Chunk8<TI>::load(x, o * D + c, v);
+      acc += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+    }
+  } else {
+    for (int64_t c = lane; c < D; c += 64) acc += Chunk8<TI>::get(x, o * D + c);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (lane == 0) Chunk8<TO>::put(out, o, acc);
+}
+
 // ---------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------
@@ -320,6 +421,51 @@ int launch_cast(const void* x, sf_dtype in, void* y, sf_dtype out, int64_t n, hi
   else if (in == SF_F16) cast_launch_i<F16>(out, x, y, n, st);
   else cast_launch_i<BF16>(out, x, y, n, st);
   return check_launch("cast");
+}
+
+// Parts S of the column sum: enough workgroups to cover the CUs twice, each
+// still summing at least 16 rows.
+int sum_dim_parts(int64_t outer, int64_t D, int64_t inner, int cus) {
+  if (inner <= 1) return 1;
+  const int64_t wgs = ((inner + 511) / 512) * outer;
+  int64_t S = (2 * (int64_t)cus + wgs - 1) / wgs;
+  if (S > D / 16) S = D / 16;
+  if (S > 1024) S = 1024;
+  return S < 1 ? 1 : (int)S;
+}
+
+template <typename TI, typename TO>
+static void sum_dim_launch_t(const void* x, void* y, int64_t outer, int64_t D, int64_t inner, float* ws, int S,
+                             hipStream_t st) {
+  if (inner == 1) {
+    const bool vec = D % 8 == 0 && aligned16(x);
+    const dim3 g(static_cast<unsigned>((outer + 3) / 4));
+    if (vec) hipLaunchKernelGGL((sum_rows_kernel<TI, TO, true>), g, dim3(256), 0, st, x, y, outer, D);
+    else hipLaunchKernelGGL((sum_rows_kernel<TI, TO, false>), g, dim3(256), 0, st, x, y, outer, D);
+    return;
+  }
+  const bool vec = inner % 8 == 0 && aligned16(x) && aligned16(y);
+  const dim3 g(static_cast<unsigned>((inner + 511) / 512), static_cast<unsigned>(S), static_cast<unsigned>(outer));
+  if (vec) hipLaunchKernelGGL((sum_cols_kernel<TI, TO, true>), g, dim3(256), 0, st, x, y, ws, D, inner, S);
+  else hipLaunchKernelGGL((sum_cols_kernel<TI, TO, false>), g, dim3(256), 0, st, x, y, ws, D, inner, S);
+  if (S > 1)
+    hipLaunchKernelGGL((sum_parts_kernel<TO>), dim3(grid_for(outer * inner)), dim3(256), 0, st, ws, y, outer, inner, S);
+}
+
+template <typename TI>
+static void sum_dim_launch_i(sf_dtype out, const void* x, void* y, int64_t outer, int64_t D, int64_t inner,
+                             float* ws, int S, hipStream_t st) {
+  if (out == SF_F32) sum_dim_launch_t<TI, float>(x, y, outer, D, inner, ws, S, st);
+  else if (out == SF_F16) sum_dim_launch_t<TI, F16>(x, y, outer, D, inner, ws, S, st);
+  else sum_dim_launch_t<TI, BF16>(x, y, outer, D, inner, ws, S, st);
+}
+
+int launch_sum_dim(const void* x, void* y, int64_t outer, int64_t D, int64_t inner, sf_dtype in, sf_dtype out,
+                   float* ws, int S, hipStream_t st) {
+  if (in == SF_F32) sum_dim_launch_i<float>(out, x, y, outer, D, inner, ws, S, st);
+  else if (in == SF_F16) sum_dim_launch_i<F16>(out, x, y, outer, D, inner, ws, S, st);
+  else sum_dim_launch_i<BF16>(out, x, y, outer, D, inner, ws, S, st);
+  return check_launch("sum_dim");
 }
 
 int launch_zero(void* p, size_t nbytes, hipStream_t st) {

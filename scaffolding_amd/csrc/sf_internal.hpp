@@ -31,13 +31,13 @@ enum TileCfg {
 const char* tile_name(int cfg);
 
 // One GEMM launch: batch entries [0, batch) of p, grid.y <= 65535 per call.
-int launch_gemm16(sf_dtype in, sf_dtype out, bool b_kmajor, int cfg, const GemmParams& p,
+int launch_gemm16(sf_dtype in, sf_dtype out, bool a_kmajor, bool b_kmajor, int cfg, const GemmParams& p,
                   int64_t batch, hipStream_t st);
-int launch_gemm16_bf16(sf_dtype out, bool b_kmajor, int cfg, const GemmParams& p, unsigned gx,
+int launch_gemm16_bf16(sf_dtype out, bool a_kmajor, bool b_kmajor, int cfg, const GemmParams& p, unsigned gx,
                        unsigned gy, hipStream_t st);
-int launch_gemm16_f16(sf_dtype out, bool b_kmajor, int cfg, const GemmParams& p, unsigned gx,
+int launch_gemm16_f16(sf_dtype out, bool a_kmajor, bool b_kmajor, int cfg, const GemmParams& p, unsigned gx,
                       unsigned gy, hipStream_t st);
-int launch_gemm32(bool b_kmajor, int cfg, const GemmParams& p, int64_t batch, hipStream_t st);
+int launch_gemm32(bool a_kmajor, bool b_kmajor, int cfg, const GemmParams& p, int64_t batch, hipStream_t st);
 
 // Tile edge of a config (BM, BN).
 void tile_dims(int cfg, bool fp32, int& bm, int& bn);
@@ -51,5 +51,10 @@ int launch_unary(int op, const void* x, void* y, int64_t n, sf_dtype dt, float s
 int launch_bias_rows(void* C, const void* bias, int64_t M, int64_t N, sf_dtype dt, hipStream_t st);
 int launch_cast(const void* x, sf_dtype in, void* y, sf_dtype out, int64_t n, hipStream_t st);
 int launch_zero(void* p, size_t nbytes, hipStream_t st);
+// Sum over the middle axis of [outer, D, inner]; S parts (sum_dim_parts)
+// with an fp32 workspace of S * outer * inner floats when S > 1.
+int sum_dim_parts(int64_t outer, int64_t D, int64_t inner, int cus);
+int launch_sum_dim(const void* x, void* y, int64_t outer, int64_t D, int64_t inner, sf_dtype in, sf_dtype out,
+                   float* ws, int S, hipStream_t st);
 
 }  // namespace sf

@@ -10,6 +10,9 @@ here independently of NumPy's BLAS:
                        (exactly rounded sums of fp64 products)
   tiny_linear.npz      tiny linear layers with bias and SiLU / GELU-tanh
                        epilogues evaluated with the math module, per element
+  tiny_backward.npz    tiny linear-layer gradients (grad_input = g W,
+                       grad_weight = g^T x, grad_bias = column sums of g)
+                       by triple loops / column loops in math.fsum
   config_inputs.json   shape, dtype and SHA-256 of every generated input of
                        BASELINE.json's five configs (oracle.configs), so the
                        generators are pinned across machines
@@ -88,6 +91,25 @@ def tiny_linear():
     np.savez(os.path.join(HERE, "tiny_linear.npz"), **arrays)
 
 
+def tiny_backward():
+    rng = np.random.default_rng(793)
+    arrays = {}
+    for dt in DTYPES:
+        for (m, n, k) in [(1, 3, 2), (5, 4, 7), (9, 6, 16), (3, 8, 5)]:
+            g = quantize(rng.uniform(-2, 2, (m, n)).astype(np.float32), dt)
+            x = quantize(rng.uniform(-2, 2, (m, k)).astype(np.float32), dt)
+            w = quantize(rng.uniform(-1, 1, (n, k)).astype(np.float32), dt)
+            key = "%s_%dx%dx%d" % (dt, m, n, k)
+            arrays[key + "_g"] = g
+            arrays[key + "_x"] = x
+            arrays[key + "_w"] = w
+            arrays[key + "_dx"] = fsum_matmul(g, w)
+            gt = np.ascontiguousarray(g.T)
+            arrays[key + "_dw"] = fsum_matmul(gt, x)
+            arrays[key + "_db"] = np.array([math.fsum(float(g[i, j]) for i in range(m)) for j in range(n)])
+    np.savez(os.path.join(HERE, "tiny_backward.npz"), **arrays)
+
+
 def digest(a: np.ndarray) -> dict:
     a = np.ascontiguousarray(a, dtype=np.float32)
     return {"shape": list(a.shape), "sha256": hashlib.sha256(a.tobytes()).hexdigest(),
@@ -114,5 +136,6 @@ def config_inputs():
 if __name__ == "__main__":
     tiny_gemm()
     tiny_linear()
+    tiny_backward()
     config_inputs()
     print("fixtures written to", HERE)

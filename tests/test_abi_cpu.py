@@ -60,7 +60,7 @@ def gemm(lib, transA=0, transB=1, M=4, N=4, K=4, batch=1, A=256, lda=4, sA=0, B=
     (dict(A=None), -2, b"null operand pointer"),
     (dict(C=None), -2, b"null operand pointer"),
     (dict(M=-1), -2, b"negative size"),
-    (dict(transA=1), -3, b"transA"),
+    (dict(transA=1, M=8, lda=4), -2, b"leading dimension"),
     (dict(ab=2, c=1), -3, b"output dtype"),
     (dict(ab=7), -2, b"unknown dtype"),
     (dict(epi=9), -2, b"unknown epilogue"),
@@ -88,6 +88,11 @@ def test_rowops_validation(lib):
     assert lib.sf_silu(None, None, I64(-1), 0, None) == -2
     assert lib.sf_cast(None, 0, None, 5, I64(1), None) == -2
     assert lib.sf_bias_add_rows(None, None, I64(2), I64(2), 0, None) == -2
+    assert lib.sf_sum_dim(None, None, I64(1), I64(4), I64(3), 0, 0, None) == -2
+    assert b"null pointer" in lib.sf_last_error()
+    assert lib.sf_sum_dim(None, None, I64(0), I64(4), I64(3), 0, 0, None) == 0
+    assert lib.sf_sum_dim(None, None, I64(1), I64(-1), I64(3), 0, 0, None) == -2
+    assert lib.sf_sum_dim(None, None, I64(1), I64(4), I64(3), 2, 1, None) == -3
 
 
 def plan(**kw):
@@ -96,7 +101,8 @@ def plan(**kw):
              ldb=4096, stride_b=0, ldc=4096, stride_c=0, dtype="bfloat16")
     a.update(kw)
     return cu.gemm_plan(a["transB"], a["M"], a["N"], a["K"], a["batch"], a["ptr_a"], a["lda"], a["stride_a"],
-                        a["ptr_b"], a["ldb"], a["stride_b"], a["ldc"], a["stride_c"], a["dtype"])
+                        a["ptr_b"], a["ldb"], a["stride_b"], a["ldc"], a["stride_c"], a["dtype"],
+                        transA=a.get("transA", 0))
 
 
 def test_dispatch_for_config_shapes():
@@ -117,6 +123,16 @@ def test_dispatch_for_config_shapes():
     # C1 / C2 fp32
     assert plan(M=64, N=512, K=512, lda=512, ldb=512, ldc=512, dtype="float32").startswith("gemm tile 64x64 fp32")
     assert plan(transB=0, dtype="float32").startswith("gemm tile 128x128 fp32")
+    # backward GEMMs: dW = dY^T X (A stored K x M) takes the register-staged
+    # tiles, never the LDS-DMA or skinny kernels; dX = dY W is NN
+    assert plan(transA=1, transB=0, M=1920, N=7680, K=17776, lda=1920, ldb=7680, ldc=7680) \
+        == "gemm tile 256x128 16-bit"
+    assert plan(transA=1, transB=0, M=1920, N=1920, K=17776, lda=1920, ldb=1920, ldc=1920) \
+        == "gemm tile 64x64 16-bit"
+    assert plan(transA=1, transB=0) == "gemm tile 256x256 16-bit"
+    assert plan(transA=1, transB=1, M=16, N=11008, ldc=11008, lda=16) == "gemm tile 64x64 16-bit"
+    assert plan(transA=1, transB=0, M=4092, lda=4092).startswith("gemm tile generic")
+    assert plan(transA=1, transB=0, dtype="float32").startswith("gemm tile 128x128 fp32")
     # unaligned operands fall back to the bounds-checked kernel
     assert plan(K=4095, lda=4095, ldb=4095).startswith("gemm tile generic")
     assert plan(ptr_a=258).startswith("gemm tile generic")

@@ -131,6 +131,56 @@ def test_linear_epilogues_against_fixtures(dt):
         assert np.allclose(y32, fx[key + "_silu"], rtol=1e-5, atol=1e-5)
 
 
+# ------------------------------------------------------------ backward
+
+def test_linear_backward_against_fixtures():
+    """LinearBackward (reference autograd.py:793-822): the fp64 closed form
+    equals the math.fsum fixtures, and the fp32 NumPy restatement is within
+    fp32 accumulation error of them."""
+    fx = np.load(os.path.join(GOLDEN, "tiny_backward.npz"))
+    keys = sorted(k[:-2] for k in fx.files if k.endswith("_g"))
+    assert len(keys) == 12
+    for key in keys:
+        g, x, w = fx[key + "_g"], fx[key + "_x"], fx[key + "_w"]
+        dx, dw, db = ref.linear_backward_f64(g, x, w)
+        np.testing.assert_allclose(dx, fx[key + "_dx"], rtol=1e-13, atol=1e-13, err_msg=key)
+        np.testing.assert_allclose(dw, fx[key + "_dw"], rtol=1e-13, atol=1e-13, err_msg=key)
+        np.testing.assert_allclose(db, fx[key + "_db"], rtol=1e-13, atol=1e-13, err_msg=key)
+        np.testing.assert_allclose(ref.matmul_tn(g.astype(np.float64), x.astype(np.float64)), fx[key + "_dw"],
+                                   rtol=1e-13, atol=1e-13)
+        np.testing.assert_allclose(ref.sum_dim(g.astype(np.float64), 0), fx[key + "_db"], rtol=1e-13, atol=1e-13)
+        gi, gw, gb = ref.linear_backward(g, x, w)
+        m = g.shape[0]
+        ag, ax, aw = (np.abs(v.astype(np.float64)) for v in (g, x, w))
+        assert np.all(np.abs(gi - fx[key + "_dx"]) <= g.shape[1] * 2.0 ** -23 * (ag @ aw) + 1e-30)
+        assert np.all(np.abs(gw - fx[key + "_dw"]) <= m * 2.0 ** -23 * (ag.T @ ax) + 1e-30)
+        assert np.all(np.abs(gb - fx[key + "_db"]) <= m * 2.0 ** -23 * ag.sum(axis=0) + 1e-30)
+        assert ref.linear_backward(g, x, w, has_bias=False)[1].shape == w.shape
+
+
+def test_backward_planted_mistakes_are_caught():
+    """A sign flip, a misaligned row pairing or a sum over the wrong axis
+    would not reproduce the fixtures."""
+    fx = np.load(os.path.join(GOLDEN, "tiny_backward.npz"))
+    key = "float32_9x6x16"
+    g, x, w = (fx[key + s].astype(np.float64) for s in ("_g", "_x", "_w"))
+    assert not np.allclose(-(g.T @ x), fx[key + "_dw"])
+    assert not np.allclose(g.T @ np.roll(x, 1, axis=0), fx[key + "_dw"])
+    assert g.sum(axis=1).shape != fx[key + "_db"].shape
+    with pytest.raises(ValueError):
+        np.matmul(g, w.T)  # grad_input with W transposed does not conform
+
+
+def test_sum_dim_shapes_follow_reference():
+    """dev_sum_dim's output shapes (reference _cuda_ops.pyx:1710-1741)."""
+    x = np.arange(24, dtype=np.float64).reshape(2, 3, 4)
+    assert ref.sum_dim(x, 1).shape == (2, 4)
+    assert ref.sum_dim(x, 1, keepdim=True).shape == (2, 1, 4)
+    assert ref.sum_dim(x, -1).shape == (2, 3)
+    assert ref.sum_dim(np.arange(5.0), 0).shape == ()  # the device op returns (1,)
+    np.testing.assert_array_equal(ref.sum_dim(x, 0), x[0] + x[1])
+
+
 # ------------------------------------------------------------ activations
 
 def test_silu_closed_forms():
