@@ -195,6 +195,21 @@ def sweep(d: Dev, steps: int, warmup: int, only: str | None):
         rec(name, ms, 2.0 * tokens * n * k, (tokens * k + n * k + tokens * n) * 2.0, "mfma", PEAK_BF16)
         del x, w
 
+    # C5 training step's backward GEMMs (next on the path after the forward):
+    # dX = dY W (NN), dW = dY^T X (TN over the 17776 tokens), db = column
+    # sums of dY, one dev_linear_backward call.  Work: 4 * tokens * N * K.
+    for pname, (k, n, has_b) in {"qkv": (1920, 5760, False), "out": (1920, 1920, True),
+                                 "mlp_up": (1920, 7680, True), "mlp_down": (7680, 1920, True)}.items():
+        name = "C5bwd_bf16_%s" % pname
+        if not want(name):
+            continue
+        x = d.rand((tokens, k), 1.0, "bfloat16")
+        w = d.rand((n, k), 0.02, "bfloat16")
+        g = d.rand((tokens, n), 1.0, "bfloat16")
+        ms = d.time_steps(lambda i: cu.dev_linear_backward(g, x, w, has_b), max(5, steps // 2), warmup)
+        rec(name, ms, 4.0 * tokens * n * k, (2 * tokens * n + 2 * tokens * k + 2 * n * k) * 2.0, "mfma", PEAK_BF16)
+        del x, w, g
+
     # Headline variant with the SiLU epilogue fused.
     if want("north_star_bias_silu"):
         x = d.rand((4096, 4096), 1.0, "bfloat16")

@@ -120,7 +120,7 @@ static int choose_tile16(int64_t M, int64_t N, int64_t K, int64_t batch, bool ve
     return (K == 2048 || K == 4096 || K == 8192) ? TILE_SKINNY_LINE : TILE_SKINNY;
   if (f32_out) return TILE_128x128;
   auto tiles = [&](int64_t bm, int64_t bn) { return cdiv(M, bm) * cdiv(N, bn) * batch; };
-  if (a_kmajor && b_kmajor && (K == 64 || (K >= 128 && K % 128 == 0)) && N > 64 && tiles(256, 256) >= cus)
+  if (((a_kmajor && b_kmajor && K == 64) || (K >= 128 && K % 128 == 0)) && N > 64 && tiles(256, 256) >= cus)
     return TILE_NT_BIG;
   if (N <= 64) return tiles(256, 64) >= cus ? TILE_256x64 : TILE_64x64;
   if (tiles(256, 256) >= cus) return TILE_256x256;
@@ -312,8 +312,10 @@ static int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K,
                      (a_kmajor || M % 8 == 0) && (b_kmajor || N % 8 == 0);
     plan.fp32 = false;
     plan.cfg = choose_tile16(M, N, K, batch, vec, a_kmajor, b_kmajor, c_dtype == SF_F32, cus);
-    // The LDS-DMA kernel addresses each operand with 32-bit byte offsets.
-    if (plan.cfg == TILE_NT_BIG && (M * lda * 2 >= (int64_t(1) << 31) || N * ldb * 2 >= (int64_t(1) << 31)))
+    // The LDS-DMA kernel addresses each operand (M or K rows of lda) with
+    // 32-bit byte offsets.
+    if (plan.cfg == TILE_NT_BIG && ((a_kmajor ? M : K) * lda * 2 >= (int64_t(1) << 31) ||
+                                    (b_kmajor ? N : K) * ldb * 2 >= (int64_t(1) << 31)))
       plan.cfg = TILE_256x256;
   }
   // The row-segment skinny kernel addresses 64 rows of W with 32-bit offsets.
@@ -392,8 +394,11 @@ int sf_gemm_plan(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
   if (!plan.noop && plan.p.split > 0)
     snprintf(extra, sizeof(extra), " split-tail %dx%d", plan.p.tiles_m * plan.p.tiles_n - plan.p.full_tiles,
              plan.p.split);
-  snprintf(buf, (size_t)len, "%s%s%s", plan.noop ? "noop" : tile_name(plan.cfg),
-           plan.noop ? "" : (plan.fp32 ? " fp32" : " 16-bit"), extra);
+  const char* name = plan.noop ? "noop" : tile_name(plan.cfg);
+  if (!plan.noop && plan.cfg == TILE_NT_BIG)  // the LDS-DMA kernel takes every operand layout
+    name = plan.a_kmajor ? (plan.b_kmajor ? "gemm nt 256x256 lds-dma" : "gemm nn 256x256 lds-dma")
+                         : (plan.b_kmajor ? "gemm tt 256x256 lds-dma" : "gemm tn 256x256 lds-dma");
+  snprintf(buf, (size_t)len, "%s%s%s", name, plan.noop ? "" : (plan.fp32 ? " fp32" : " 16-bit"), extra);
   return SF_OK;
 }
 

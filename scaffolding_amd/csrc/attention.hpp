@@ -43,16 +43,6 @@ struct AttnParams {
   float scale_log2e;           // scale * log2(e)
 };
 
-// ds_read_b64_tr_b16 as inline assembly (see ds_read16 for why): within each
-// 16-lane group, lane 4a + b receives element b of the 8-byte rows addressed
-// by lanes a, 4 + a, 8 + a and 12 + a (measured lane layout).
-template <int OFF>
-__device__ __forceinline__ u32x2 ds_read_tr16(uint32_t addr) {
-  u32x2 v;
-  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
-  return v;
-}
-
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
 template <typename T>

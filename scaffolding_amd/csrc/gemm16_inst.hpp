@@ -51,13 +51,14 @@ static int launch16_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hi
       break;
     case TILE_NT_BIG:
       if constexpr (KM && AKM) {
-        if (p.K == 64)
+        if (p.K == 64) {
           hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut, 1>), g, dim3(512), 0, st, p);
-        else
-          hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut, 2>), g, dim3(512), 0, st, p);
-        break;
+          break;
+        }
       }
-      return fail(SF_ERR_UNSUPPORTED, "the 256x256 NT kernel needs K-contiguous A and B");
+      if (p.K % 128 != 0) return fail(SF_ERR_INVALID_ARG, "the 256x256 LDS-DMA kernel needs K %% 128 == 0");
+      hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut, 2, AKM, KM>), g, dim3(512), 0, st, p);
+      break;
     case TILE_SKINNY:
       if constexpr (KM && AKM) {
         // grid.x = ceil(N / 32): 2 row blocks per workgroup, K split over 4 waves.

@@ -1,8 +1,11 @@
-// gemm16nt_pp.hpp — large-problem 16-bit NT GEMM with an 8-wave ping-pong
+// gemm16nt_pp.hpp — large-problem 16-bit GEMM with an 8-wave ping-pong
 // schedule:
 //
-//   C[b] = epi(alpha * A[b] . B[b]^T (+ bias)),  A M x K, B N x K, both
-//   K-contiguous, 16-bit in and out, fp32 accumulation.
+//   C[b] = epi(alpha * op(A[b]) . op(B[b]) (+ bias)),  16-bit in and out,
+//   fp32 accumulation.  Each operand is K-contiguous (A M x K, B N x K: the
+//   forward "NT" product x . W^T) or M/N-contiguous (A stored K x M, B stored
+//   K x N: the backward products dY . W and dY^T . X) — template flags
+//   A_KM / B_KM.
 //
 // One 512-thread workgroup per 256 x 256 output tile; eight waves in a
 // 2 x 4 grid, each owning a 128 x 64 sub-tile = 4 x 8 blocks of
@@ -30,6 +33,18 @@
 // useful bytes per request of 64-byte row halves.  Rows past M or N are
 // clamped to the last valid row (their products only reach unstored
 // outputs); K % 128 == 0 is required.
+//
+// M/N-contiguous operands.  The stage (same 32 KB per operand) holds four
+// blocks of 64 m (or n); block b is 64 k-rows of 128 bytes (64 m of one k),
+// 16-byte chunk c of row k at slot c ^ fmn(k), fmn(k) = 2 ((k >> 1) & 1) +
+// 4 ((k >> 3) & 1).  Direct-load instruction i of wave w fills rows
+// 8w .. 8w+7 of block i (whole 128-byte rows again).  Fragments come from
+// gfx950's transposing read ds_read_b64_tr_b16: two reads (k 0-3 and 4-7 of
+// the lane group's 8) give a lane the same 8 k of its m that a ds_read_b128
+// gives from a K-contiguous tile, and the swizzle spreads the 16 rows each
+// read touches over distinct banks (0 SQ_LDS_BANK_CONFLICT, measured).
+// Columns past M or N read neighbouring data or, past the buffer's end,
+// zeros; their products only reach unstored outputs.
 //
 // Schedule per slice t (group 0 between barriers 2t and 2t+1, group 1 one
 // barrier later): at even t each wave issues its loads of pair t/2 + 1 into
@@ -61,6 +76,16 @@ template <int OFF>
 __device__ __forceinline__ u32x4 ds_read16(uint32_t addr) {
   u32x4 v;
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+
+// ds_read_b64_tr_b16 as inline assembly (as ds_read16): within each 16-lane
+// group, lane 4a + b receives element b of the 8-byte rows addressed by
+// lanes a, 4 + a, 8 + a and 12 + a (measured lane layout).
+template <int OFF>
+__device__ __forceinline__ u32x2 ds_read_tr16(uint32_t addr) {
+  u32x2 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
   return v;
 }
 
@@ -102,9 +127,10 @@ constexpr int waitcnt_imm(int vm, int lgkm) {
 // exactly (one slice pair, e.g. attention scores Q.K^T at head size 64): a
 // single 64 KB stage, so two workgroups share a CU and one's stores overlap
 // the other's loads.
-template <typename TIn, typename TOut, int NSTAGE = 2>
+template <typename TIn, typename TOut, int NSTAGE = 2, bool A_KM = true, bool B_KM = true>
 __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   static_assert(NSTAGE == 1 || NSTAGE == 2, "one or two pair stages");
+  static_assert(NSTAGE == 2 || (A_KM && B_KM), "K == 64 stage: K-contiguous operands only");
   constexpr int BM = 256, BN = 256, BK = 32;
   constexpr int WM = 128, WN = 64, FM = WM / 16, FN = WN / 16;
   constexpr int OP_BYTES = BM * 2 * BK * 2;  // 32 KB: one operand, two slices
@@ -166,31 +192,74 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   // of the pair is chunks 0-3, slice 2s+1 chunks 4-7.  Direct loads fetch
   // whole 128-byte rows: instruction i of this wave fills lines wave*32 +
   // 8 i .. +7, lane l line + (l >> 3), slot l & 7, i.e. chunk (l&7)^(l>>3).
+  // An M/N-contiguous operand: instruction i fills rows 8 wave .. +7 of
+  // block i (stage bytes i * 8192 + wave * 1024 ..), lane l row
+  // 8 wave + (l >> 3), slot l & 7, i.e. chunk (l & 7) ^ fmn(8 wave + (l >> 3)).
   const int dh = (lane & 7) ^ (lane >> 3);
   const uint32_t dchunk_b = (uint32_t)(dh * 16);
   const int drow = wave * 32 + (lane >> 3);
+  const int mrow = wave * 8 + (lane >> 3);  // k-row of an M/N-contiguous operand
+  const int mch = (lane & 7) ^ (2 * ((mrow >> 1) & 1) + 4 * ((mrow >> 3) & 1));
   // Buffer resources over A's and B's rows of this batch; per-lane 32-bit
   // row offsets (rows past M / N clamped to the last row: their products
   // only reach unstored outputs) are fixed for the whole loop, the k offset
   // goes in the scalar offset.  Every byte read lies below rows * ld * 2.
+  const uint32_t a_rows = A_KM ? (uint32_t)M : (uint32_t)K;
+  const uint32_t b_rows = B_KM ? (uint32_t)N : (uint32_t)K;
   const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)A, (short)0, (int)((uint32_t)M * (uint32_t)p.lda * 2u), 0x00020000);
+      (void*)A, (short)0, (int)(a_rows * (uint32_t)p.lda * 2u), 0x00020000);
   const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)B, (short)0, (int)((uint32_t)N * (uint32_t)p.ldb * 2u), 0x00020000);
-  uint32_t voa[DMA_I], vob[DMA_I];
-#pragma unroll
-  for (int i = 0; i < DMA_I; ++i) {
-    const int ga = m0 + drow + i * 8, gb = n0 + drow + i * 8;
-    voa[i] = (uint32_t)(ga < M ? ga : M - 1) * (uint32_t)p.lda * 2u + dchunk_b;
-    vob[i] = (uint32_t)(gb < N ? gb : N - 1) * (uint32_t)p.ldb * 2u + dchunk_b;
-  }
-  auto dma = [&](uint8_t* sA, uint8_t* sB, int k0) {
-    const int so = (t_begin * BK + k0) * 2;
+      (void*)B, (short)0, (int)(b_rows * (uint32_t)p.ldb * 2u), 0x00020000);
+  // An M/N-contiguous operand needs one per-lane offset: instruction i
+  // reads 64 columns (128 bytes) further, through the instruction's
+  // immediate offset.  That offset also moves the LDS destination, so the
+  // LDS base handed to the instruction is lowered by the same amount.
+  uint32_t voa[A_KM ? DMA_I : 1], vob[B_KM ? DMA_I : 1];
+  if constexpr (A_KM) {
 #pragma unroll
     for (int i = 0; i < DMA_I; ++i) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_ptr_t)(sA + (wave * 32 + i * 8) * 128), 16, voa[i], so, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_ptr_t)(sB + (wave * 32 + i * 8) * 128), 16, vob[i], so, 0, 0);
+      const int ga = m0 + drow + i * 8;
+      voa[i] = (uint32_t)(ga < M ? ga : M - 1) * (uint32_t)p.lda * 2u + dchunk_b;
     }
+  } else {
+    voa[0] = ((uint32_t)mrow * (uint32_t)p.lda + (uint32_t)(m0 + mch * 8)) * 2u;
+  }
+  if constexpr (B_KM) {
+#pragma unroll
+    for (int i = 0; i < DMA_I; ++i) {
+      const int gb = n0 + drow + i * 8;
+      vob[i] = (uint32_t)(gb < N ? gb : N - 1) * (uint32_t)p.ldb * 2u + dchunk_b;
+    }
+  } else {
+    vob[0] = ((uint32_t)mrow * (uint32_t)p.ldb + (uint32_t)(n0 + mch * 8)) * 2u;
+  }
+  // With an M/N-contiguous operand beside it, a K-contiguous operand keeps
+  // only its first row offset live and adds the 8-row steps at issue time
+  // (the empty asm hides the value's invariance from loop hoisting): the
+  // kernel then fits in 256 VGPRs without spills.
+  constexpr bool LEAN = !(A_KM && B_KM);
+  auto dma_op = [&](auto km_c, const __amdgpu_buffer_rsrc_t& rs, uint8_t* st, uint32_t* vo, int so, uint32_t step8) {
+    constexpr bool KMJ = decltype(km_c)::value;
+    if constexpr (KMJ && LEAN) asm volatile("" : "+v"(vo[0]));
+    static_for<DMA_I>([&](auto i_c) {
+      constexpr int I = decltype(i_c)::value;
+      if constexpr (KMJ && LEAN)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(st + wave * 4096 + I * 1024), 16,
+                                                 vo[0] + (uint32_t)I * step8, so, 0, 0);
+      else if constexpr (KMJ)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(st + wave * 4096 + I * 1024), 16, vo[I], so, 0, 0);
+      else  // the k-row offset goes in the lane offset, so the buffer's bound
+            // check covers it: columns past the last row's end read zeros.
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(st + wave * 1024 + I * (8192 - 128)), 16,
+                                                 vo[0] + (uint32_t)so, 0, I * 128, 0);
+    });
+  };
+  auto dma = [&](uint8_t* sA, uint8_t* sB, int k0) {
+    const int kk = t_begin * BK + k0;  // first k of the pair
+    dma_op(std::integral_constant<bool, A_KM>{}, rA, sA, voa, A_KM ? kk * 2 : kk * (int)p.lda * 2,
+           (uint32_t)p.lda * 16u);
+    dma_op(std::integral_constant<bool, B_KM>{}, rB, sB, vob, B_KM ? kk * 2 : kk * (int)p.ldb * 2,
+           (uint32_t)p.ldb * 16u);
   };
 
   f32x4 acc[FN][FM];
@@ -200,29 +269,52 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
     for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   u32x4 ya[FM], xb[FN];
 
-  // Fragment byte offsets for slice half 0: A block j reads lines wm*128 +
-  // 16 j + (l & 15), chunk l >> 4; B block i lines wn*64 + 16 i + (l & 15).
-  // Half 1 reads chunk 4 + (l >> 4): its slot differs in bit 2 (byte bit 6).
+  // Fragment byte offsets for slice half 0 of a K-contiguous operand: A
+  // block j reads lines wm*128 + 16 j + (l & 15), chunk l >> 4; B block i
+  // lines wn*64 + 16 i + (l & 15).  Half 1 reads chunk 4 + (l >> 4): its
+  // slot differs in bit 2 (byte bit 6).
   const int fa = (wm * 128 + (lane & 15)) * 128 + (((lane >> 4) ^ (lane & 7)) << 4);
   const int fb = (wn * 64 + (lane & 15)) * 128 + (((lane >> 4) ^ (lane & 7)) << 4);
+  // M/N-contiguous operand, lane l = 16 g + 4 e + a: the transposing read
+  // of 8 bytes at k-row 8 g + e (+ 4 for k 4-7, + 32 for the second slice),
+  // columns 16 j + 4 a .. + 3, i.e. chunk 2 j + (a >> 1) at slot
+  // (2 j + (a >> 1)) ^ fmn(k); fmn of these rows is 2 ((e >> 1) & 1) +
+  // 4 (g & 1) for every half and slice, so fragment j' = j % 4 is the base
+  // address with (j' << 5) xor-ed in, and j / 4 selects the 8 KB block.
+  const int mn_g = lane >> 4, mn_e = (lane >> 2) & 3, mn_a = lane & 3;
+  const int mn_f = 2 * ((mn_e >> 1) & 1) + 4 * (mn_g & 1);
+  const int fmn = (8 * mn_g + mn_e) * 128 + ((mn_f | (mn_a >> 1)) << 4) + (mn_a & 1) * 8;
+  const int fa_mn = (2 * wm) * 8192 + fmn;  // A: blocks 2 wm, 2 wm + 1
+  const int fb_mn = wn * 8192 + fmn;        // B: block wn
+
+  // One fragment of a K-contiguous operand (one ds_read_b128) or of an
+  // M/N-contiguous one (two transposing reads, k 0-3 then 4-7).
+  auto frag_km = [&](auto j_c, uint32_t base) -> u32x4 {
+    constexpr int J = decltype(j_c)::value;
+    return ds_read16<J * 2048>(base);
+  };
+  auto frag_mn = [&](auto j_c, uint32_t base) -> u32x4 {
+    constexpr int J = decltype(j_c)::value;
+    const uint32_t ad = base ^ (uint32_t)((J & 3) << 5);
+    const u32x2 lo = ds_read_tr16<(J >> 2) * 8192>(ad);
+    const u32x2 hi = ds_read_tr16<(J >> 2) * 8192 + 512>(ad);
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
+  };
 
   auto step = [&](int t, const uint8_t* sA, const uint8_t* sB, uint8_t* nA, uint8_t* nB) {
     const bool odd = t & 1;  // static after unrolling
     // memory phase
     __builtin_amdgcn_sched_barrier(0);
-    const uint32_t la = lds_addr(sA) + (odd ? (fa ^ 64) : fa), lb = lds_addr(sB) + (odd ? (fb ^ 64) : fb);
-    ya[0] = ds_read16<0 * 2048>(la);
-    ya[1] = ds_read16<1 * 2048>(la);
-    ya[2] = ds_read16<2 * 2048>(la);
-    ya[3] = ds_read16<3 * 2048>(la);
-    ya[4] = ds_read16<4 * 2048>(la);
-    ya[5] = ds_read16<5 * 2048>(la);
-    ya[6] = ds_read16<6 * 2048>(la);
-    ya[7] = ds_read16<7 * 2048>(la);
-    xb[0] = ds_read16<0 * 2048>(lb);
-    xb[1] = ds_read16<1 * 2048>(lb);
-    xb[2] = ds_read16<2 * 2048>(lb);
-    xb[3] = ds_read16<3 * 2048>(lb);
+    const uint32_t la = A_KM ? lds_addr(sA) + (odd ? (fa ^ 64) : fa) : lds_addr(sA) + fa_mn + (odd ? 4096 : 0);
+    const uint32_t lb = B_KM ? lds_addr(sB) + (odd ? (fb ^ 64) : fb) : lds_addr(sB) + fb_mn + (odd ? 4096 : 0);
+    static_for<FM>([&](auto j_c) {
+      if constexpr (A_KM) ya[decltype(j_c)::value] = frag_km(j_c, la);
+      else ya[decltype(j_c)::value] = frag_mn(j_c, la);
+    });
+    static_for<FN>([&](auto i_c) {
+      if constexpr (B_KM) xb[decltype(i_c)::value] = frag_km(i_c, lb);
+      else xb[decltype(i_c)::value] = frag_mn(i_c, lb);
+    });
     // Even t: the other pair stage was last read in step t-1, which both
     // groups finished before this phase; fill it with pair t/2 + 1.
     if (!odd && t / 2 + 1 < KP) dma(nA, nB, (t + 2) * BK);

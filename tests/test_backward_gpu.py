@@ -185,3 +185,77 @@ def test_linear_backward_training_shape():
     check_bound(dw, dw64, gemm_bound(dw64, np.abs(g64[:, rows]).T @ np.abs(x64), m, "bfloat16"), "dW")
     db64, bound = _sum_bound(g64, 0, "bfloat16")
     check_bound(down(gb), db64, bound, "db")
+
+
+LDS_DMA_CASES = [
+    # (dtype, transA, transB, M, N, K, batch, epilogue, expected plan)
+    ("bfloat16", 0, 0, 4096, 4096, 256, 1, 0, "gemm nn 256x256 lds-dma"),
+    ("float16", 1, 0, 4000, 4104, 384, 1, 0, "gemm tn 256x256 lds-dma"),
+    ("bfloat16", 1, 1, 4096, 4096, 128, 1, 0, "gemm tt 256x256 lds-dma"),
+    ("float16", 0, 0, 1000, 1104, 128, 16, 0, "gemm nn 256x256 lds-dma"),
+    ("bfloat16", 1, 0, 1000, 1104, 256, 16, 0, "gemm tn 256x256 lds-dma"),
+    ("bfloat16", 1, 0, 4352, 4096, 1024, 1, 0, "gemm tn 256x256 lds-dma 16-bit split-tail 16x8"),
+    ("bfloat16", 0, 0, 4352, 4096, 1024, 1, 1, "gemm nn 256x256 lds-dma 16-bit split-tail 16x8"),
+    ("bfloat16", 0, 0, 2104, 8000, 512, 1, 3, "gemm nn 256x256 lds-dma"),
+    ("float16", 1, 0, 2104, 8000, 512, 1, 2, "gemm tn 256x256 lds-dma"),
+]
+
+
+@pytest.mark.parametrize("case", LDS_DMA_CASES, ids=lambda c: "%s-%s%s-%dx%dx%dx%d-e%d" % (
+    c[0], "T" if c[1] else "N", "T" if c[2] else "N", c[3], c[4], c[5], c[6], c[7]))
+def test_lds_dma_layouts(case):
+    """The 256x256 LDS-DMA kernel with M/N-contiguous operands (transposing
+    fragment reads), ragged edges, batches, the split tail and epilogues,
+    through the C ABI: sampled rows against fp64 plus row and column
+    checksums of the whole output."""
+    dtype, ta, tb, m, n, k, batch, epi, expect = case
+    rng = np.random.default_rng(9000 + m + n + k + 10 * ta + tb + batch)
+    shp = lambda *s: ((batch,) if batch > 1 else ()) + s  # noqa: E731
+    a = rnd(rng, shp(k, m) if ta else shp(m, k), 1.0, dtype)
+    b = rnd(rng, shp(n, k) if tb else shp(k, n), 1.0 / np.sqrt(k), dtype)
+    bias = rnd(rng, (n,), 0.5, dtype)
+    ga, gb, gbias = up(a, dtype), up(b, dtype), up(bias, dtype)
+    lda, ldb = (m if ta else k), (k if tb else n)
+    plan = cu().gemm_plan(tb, m, n, k, batch, ga.data_ptr, lda, m * k if batch > 1 else 0, gb.data_ptr, ldb,
+                          n * k if batch > 1 else 0, n, m * n, ga.dtype, epi=epi,
+                          ptr_bias=gbias.data_ptr if epi in (1, 2, 3) else 0, transA=ta)
+    assert plan.startswith(expect), plan
+    gc = cu().empty(shp(m, n), ga.dtype, 0)
+    I64 = ctypes.c_int64
+    lib = _lib()
+    rc = lib.sf_gemm(ta, tb, I64(m), I64(n), I64(k), I64(batch), ctypes.c_void_p(ga.data_ptr), I64(lda),
+                     I64(m * k if batch > 1 else 0), ctypes.c_void_p(gb.data_ptr), I64(ldb),
+                     I64(n * k if batch > 1 else 0), ctypes.c_void_p(gc.data_ptr), I64(n), I64(m * n), SFD[dtype],
+                     SFD[dtype], ctypes.c_float(1.0), ctypes.c_void_p(gbias.data_ptr if epi in (1, 2, 3) else None),
+                     epi, None)
+    assert rc == 0, lib.sf_last_error()
+    cu().device_synchronize()
+    y = down(gc).reshape(batch, m, n)
+    a3 = a.reshape((batch, k, m) if ta else (batch, m, k)).astype(np.float64)
+    b3 = b.reshape((batch, n, k) if tb else (batch, k, n)).astype(np.float64)
+    am = np.swapaxes(a3, -2, -1) if ta else a3
+    bm = np.swapaxes(b3, -2, -1) if tb else b3
+    act = {0: None, 1: None, 2: "silu", 3: "gelu"}[epi]
+    rows = np.unique(np.r_[0, m - 1, np.arange(0, m, 97), np.arange(255, m, 256), np.arange(256, m, 256)])
+    for bi in sorted({0, batch - 1}):
+        pre = am[bi, rows] @ bm[bi] + (bias.astype(np.float64) if epi else 0.0)
+        y64 = ref.act_f64(pre, act)
+        absprod = np.abs(am[bi, rows]) @ np.abs(bm[bi]) + (np.abs(bias.astype(np.float64)) if epi else 0.0)
+        check_bound(y[bi, rows], y64, gemm_bound(y64, absprod, k, dtype, act), "%s rows" % (case,))
+        if epi == 0:
+            rs = y[bi].astype(np.float64).sum(axis=1)
+            cs = y[bi].astype(np.float64).sum(axis=0)
+            full_abs = np.abs(am[bi]) @ np.abs(bm[bi])
+            eps = 2 * (k * 2.0 ** -23 + {"float16": 2.0 ** -11, "bfloat16": 2.0 ** -8}[dtype])
+            assert np.all(np.abs(rs - am[bi] @ bm[bi].sum(axis=1)) <= eps * full_abs.sum(axis=1) + 1e-6)
+            assert np.all(np.abs(cs - am[bi].sum(axis=0) @ bm[bi]) <= eps * full_abs.sum(axis=0) + 1e-6)
+
+
+def test_lds_dma_split_tail_is_deterministic():
+    rng = np.random.default_rng(31)
+    m, n, k = 4352, 4096, 1024
+    a = up(rnd(rng, (k, m), 1.0, "bfloat16"), "bfloat16")
+    b = up(rnd(rng, (k, n), 0.03, "bfloat16"), "bfloat16")
+    y1 = cu().gputensor_bits_to_numpy(cu().dev_matmul_tn(a, b))
+    y2 = cu().gputensor_bits_to_numpy(cu().dev_matmul_tn(a, b))
+    assert np.array_equal(y1, y2)
