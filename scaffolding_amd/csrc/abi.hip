@@ -120,8 +120,15 @@ static int choose_tile16(int64_t M, int64_t N, int64_t K, int64_t batch, bool ve
     return (K == 2048 || K == 4096 || K == 8192) ? TILE_SKINNY_LINE : TILE_SKINNY;
   if (f32_out) return TILE_128x128;
   auto tiles = [&](int64_t bm, int64_t bn) { return cdiv(M, bm) * cdiv(N, bn) * batch; };
-  if (((a_kmajor && b_kmajor && K == 64) || (K >= 128 && K % 128 == 0)) && N > 64 && tiles(256, 256) >= cus)
-    return TILE_NT_BIG;
+  // The LDS-DMA kernel: K-contiguous operands need K % 128 == 0 (or K == 64
+  // for NT); two M/N-contiguous operands take any K >= 128.  It runs at
+  // least half a wave of 256 x 256 tiles, or fewer for a single GEMM whose
+  // tiles the split below cuts along k.
+  const bool k_ok = (a_kmajor && b_kmajor && K == 64) || (K >= 128 && (K % 128 == 0 || (!a_kmajor && !b_kmajor)));
+  const int64_t t256 = tiles(256, 256);
+  const bool fills = t256 >= cus || (!(a_kmajor && b_kmajor) && M > 64 &&
+                                     (2 * t256 >= cus || (batch == 1 && K >= 1024 && 16 * t256 >= cus)));
+  if (k_ok && N > 64 && fills) return TILE_NT_BIG;
   if (N <= 64) return tiles(256, 64) >= cus ? TILE_256x64 : TILE_64x64;
   if (tiles(256, 256) >= cus) return TILE_256x256;
   if (tiles(256, 128) >= cus) return TILE_256x128;
@@ -331,11 +338,12 @@ static int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K,
   p.split = 0;
   p.ws = nullptr;
   p.counters = nullptr;
-  if (plan.cfg == TILE_NT_BIG && batch == 1 && K % 128 == 0) {
+  if (plan.cfg == TILE_NT_BIG && batch == 1 && K >= 128) {
     // Tail split: with R = tiles % CUs left over after whole waves, run the
     // last R tiles as R * s workgroups of K / s each (s <= CUs / R), so the
-    // last wave is full instead of R / CUs full.
-    const int64_t T = (int64_t)p.tiles_m * p.tiles_n, R = T % cus, units = K / 128;
+    // last wave is full instead of R / CUs full.  With fewer tiles than
+    // half the CUs every tile is split (split-K).
+    const int64_t T = (int64_t)p.tiles_m * p.tiles_n, R = T % cus, units = (K + 127) / 128;
     if (R > 0 && 2 * R <= cus && units >= 2) {
       int64_t sp = cus / R;
       if (sp > units) sp = units;

@@ -56,7 +56,8 @@ static int launch16_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hi
           break;
         }
       }
-      if (p.K % 128 != 0) return fail(SF_ERR_INVALID_ARG, "the 256x256 LDS-DMA kernel needs K %% 128 == 0");
+      if (p.K % 128 != 0 && (AKM || KM))
+        return fail(SF_ERR_INVALID_ARG, "the 256x256 LDS-DMA kernel needs K %% 128 == 0 with a K-contiguous operand");
       hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut, 2, AKM, KM>), g, dim3(512), 0, st, p);
       break;
     case TILE_SKINNY:

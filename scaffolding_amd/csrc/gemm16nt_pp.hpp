@@ -44,7 +44,9 @@
 // gives from a K-contiguous tile, and the swizzle spreads the 16 rows each
 // read touches over distinct banks (0 SQ_LDS_BANK_CONFLICT, measured).
 // Columns past M or N read neighbouring data or, past the buffer's end,
-// zeros; their products only reach unstored outputs.
+// zeros; their products only reach unstored outputs.  With both operands
+// M/N-contiguous, K may be any multiple of 8: k-rows past K lie beyond both
+// buffers' bounds and read as zeros, so they add nothing.
 //
 // Schedule per slice t (group 0 between barriers 2t and 2t+1, group 1 one
 // barrier later): at even t each wave issues its loads of pair t/2 + 1 into
@@ -148,7 +150,11 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   int tm, tn;
   // This workgroup's k slices [t_begin, t_begin + KT) and, in a split tile,
   // its part index (-1: whole tile).
-  int t_begin = 0, KT = K / BK, part = -1, split_tile = 0;
+  // With two M/N-contiguous operands K need not be a multiple of 128: the
+  // loop runs to the next multiple and the k-rows past K read as zeros
+  // through both buffers' bounds.
+  const int KU = (K + 4 * BK - 1) / (4 * BK);  // 128-k units
+  int t_begin = 0, KT = NSTAGE == 2 ? 4 * KU : K / BK, part = -1, split_tile = 0;
   {
     int pid;
     int spid = -1;  // split part id
@@ -170,7 +176,7 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
     }
     if (spid >= 0) {
       const int r = spid / p.split, q = spid % p.split;
-      const int units = K / (4 * BK);  // 128-k units
+      const int units = KU;
       const int u0 = q * units / p.split, u1 = (q + 1) * units / p.split;
       t_begin = 4 * u0;
       KT = 4 * (u1 - u0);

@@ -126,13 +126,14 @@ def test_dispatch_for_config_shapes():
     # backward GEMMs: dW = dY^T X (A stored K x M) takes the register-staged
     # tiles, never the LDS-DMA or skinny kernels; dX = dY W is NN
     assert plan(transA=1, transB=0, M=1920, N=7680, K=17776, lda=1920, ldb=7680, ldc=7680) \
-        == "gemm tile 256x128 16-bit"
+        == "gemm tn 256x256 lds-dma 16-bit"
     assert plan(transA=1, transB=0, M=1920, N=1920, K=17776, lda=1920, ldb=1920, ldc=1920) \
-        == "gemm tile 64x64 16-bit"
+        == "gemm tn 256x256 lds-dma 16-bit split-tail 64x4"
     assert plan(transA=1, transB=0, ldb=4096) == "gemm tn 256x256 lds-dma 16-bit"
     assert plan(transA=0, transB=0, ldb=4096) == "gemm nn 256x256 lds-dma 16-bit"
     assert plan(transA=1, transB=1) == "gemm tt 256x256 lds-dma 16-bit"
-    assert plan(transA=1, transB=0, ldb=4096, K=4000) == "gemm tile 256x256 16-bit"  # K % 128 != 0
+    assert plan(transA=1, transB=0, ldb=4096, K=4000) == "gemm tn 256x256 lds-dma 16-bit"  # any K for TN
+    assert plan(transA=0, transB=0, ldb=4096, K=4000) == "gemm tile 256x256 16-bit"  # K % 128 != 0
     assert plan(transA=1, transB=1, M=16, N=11008, ldc=11008, lda=16) == "gemm tile 64x64 16-bit"
     assert plan(transA=1, transB=0, M=4092, lda=4092).startswith("gemm tile generic")
     assert plan(transA=1, transB=0, dtype="float32").startswith("gemm tile 128x128 fp32")
