@@ -251,14 +251,28 @@ __global__ __launch_bounds__(256) void sum_cols_kernel(const void* __restrict__ 
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
   if (i0 < inner) {
     const int64_t base = o * D * inner + i0;
-    for (int64_t d = d0 + wave; d < d1; d += 4) {
-      float v[8];
+    auto ld = [&](int64_t d, float v[8]) {
       if constexpr (VEC) {
         Chunk8<TI>::load(x, base + d * inner, v);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = (i0 + e < inner) ? Chunk8<TI>::get(x, base + d * inner + e) : 0.f;
       }
+    };
+    int64_t d = d0 + wave;
+    // Four rows' loads in flight per wave, added in row order.
+    for (; d + 12 < d1; d += 16) {
+      float v0[8], v1[8], v2[8], v3[8];
+      ld(d, v0);
+      ld(d + 4, v1);
+      ld(d + 8, v2);
+      ld(d + 12, v3);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = (((acc[e] + v0[e]) + v1[e]) + v2[e]) + v3[e];
+    }
+    for (; d < d1; d += 4) {
+      float v[8];
+      ld(d, v);
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] += v[e];
     }
@@ -288,17 +302,33 @@ __global__ __launch_bounds__(256) void sum_cols_kernel(const void* __restrict__ 
   }
 }
 
+// Adds the S partials of each output in part order, 64 outputs per
+// workgroup: the 4 waves add parts s = w, w + 4, ... (eight loads in
+// flight), then wave 0 adds the four wave sums in wave order.
 template <typename TO>
 __global__ __launch_bounds__(256) void sum_parts_kernel(const float* __restrict__ ws, void* __restrict__ out,
                                                         int64_t outer, int64_t inner, int S) {
-  const int64_t n = outer * inner;
-  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < n; idx += (int64_t)gridDim.x * 256) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t idx = (int64_t)blockIdx.x * 64 + lane;
+  float t = 0.f;
+  if (idx < outer * inner) {
     const int64_t o = idx / inner, i = idx - o * inner;
     const float* w = ws + o * S * inner + i;
-    float t = 0.f;
-    for (int s = 0; s < S; ++s) t += w[(int64_t)s * inner];
-    Chunk8<TO>::put(out, idx, t);
+    int s = wave;
+    for (; s + 28 < S; s += 32) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = w[(int64_t)(s + 4 * u) * inner];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t += v[u];
+    }
+    for (; s < S; s += 4) t += w[(int64_t)s * inner];
   }
+  __shared__ float red[4][64];
+  red[wave][lane] = t;
+  __syncthreads();
+  if (wave == 0 && idx < outer * inner)
+    Chunk8<TO>::put(out, idx, ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane]);
 }
 
 template <typename TI, typename TO, bool VEC>
@@ -423,13 +453,13 @@ int launch_cast(const void* x, sf_dtype in, void* y, sf_dtype out, int64_t n, hi
   return check_launch("cast");
 }
 
-// Parts S of the column sum: enough workgroups to cover the CUs twice, each
-// still summing at least 16 rows.
+// Parts S of the column sum: enough workgroups to cover the CUs once, each
+// still summing at least 64 rows.
 int sum_dim_parts(int64_t outer, int64_t D, int64_t inner, int cus) {
   if (inner <= 1) return 1;
   const int64_t wgs = ((inner + 511) / 512) * outer;
-  int64_t S = (2 * (int64_t)cus + wgs - 1) / wgs;
-  if (S > D / 16) S = D / 16;
+  int64_t S = ((int64_t)cus + wgs - 1) / wgs;
+  if (S > D / 64) S = D / 64;
   if (S > 1024) S = 1024;
   return S < 1 ? 1 : (int)S;
 }
@@ -449,7 +479,8 @@ static void sum_dim_launch_t(const void* x, void* y, int64_t outer, int64_t D, i
   if (vec) hipLaunchKernelGGL((sum_cols_kernel<TI, TO, true>), g, dim3(256), 0, st, x, y, ws, D, inner, S);
   else hipLaunchKernelGGL((sum_cols_kernel<TI, TO, false>), g, dim3(256), 0, st, x, y, ws, D, inner, S);
   if (S > 1)
-    hipLaunchKernelGGL((sum_parts_kernel<TO>), dim3(grid_for(outer * inner)), dim3(256), 0, st, ws, y, outer, inner, S);
+    hipLaunchKernelGGL((sum_parts_kernel<TO>), dim3(static_cast<unsigned>((outer * inner + 63) / 64)), dim3(256), 0, st,
+                       ws, y, outer, inner, S);
 }
 
 template <typename TI>
