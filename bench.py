@@ -74,8 +74,17 @@ class Dev:
                 keep.pop(0)
         cu.device_synchronize()
         e0, e1 = cu.CudaEvent(), cu.CudaEvent()
+        e0.record()
+        e0.synchronize()
         gc.disable()
         try:
+            # A few untimed calls queue work ahead of the start event, so the
+            # GPU is busy when it records and host-side launch latency does
+            # not open an idle gap inside the timed region.
+            for i in range(4):
+                keep.append(fn(i))
+                if len(keep) > 8:
+                    keep.pop(0)
             e0.record()
             for i in range(steps):
                 keep.append(fn(i))

@@ -117,6 +117,17 @@ __global__ __launch_bounds__(KSPLIT * 64) void skinny16_kernel(GemmParams p) {
 }
 
 
+// 16-byte global load issued as inline assembly at byte offset OFF, with no
+// wait: the caller orders it with an explicit s_waitcnt and then tie2.
+template <int OFF>
+__device__ __forceinline__ u32x4 gload16_nowait(const void* p) {
+  u32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(v) : "v"(p), "i"(OFF) : "memory");
+  return v;
+}
+// Marks both registers as written here, so no use moves above this point.
+__device__ __forceinline__ void tie2(u32x4& a, u32x4& b) { asm volatile("" : "+v"(a), "+v"(b)); }
+
 // skinny16l_kernel — the M <= 16 stream for K = 512 * NW (NW waves), reading
 // W in whole 128-byte row segments.
 //
@@ -177,18 +188,33 @@ __global__ __launch_bounds__(NW * 64) void skinny16l_kernel(GemmParams p) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rW, (lds_ptr_t)(dst + 1024), 16, v0 + 8u * ldb_b, L * 128, 0,
                                              kNonTemporal);
   };
-  static_for<R - 1>([&](auto Lc) { issue(0, Lc); });
-
   // x fragments: slice s (k = kw + 32 s ..) lane l: row m = l & 15, 8 k at
-  // kw + 32 s + 8 (l >> 4); rows past M are zero.
+  // kw + 32 s + 8 (l >> 4); rows past M are zero.  Tile L of the first row
+  // block brings the two slices it needs (2 L, 2 L + 1) right after its W
+  // loads, so x (16 KB per wave at M = 16) streams beside W instead of
+  // holding the load path before W starts.
+  // The x loads are inline assembly: the compiler would count only them
+  // (not the direct loads between them) when it places its own wait before
+  // an MFMA that uses them, and so wait for more W tiles than needed.  The
+  // explicit waits below count them, and xtie marks the registers as written
+  // after that wait, so nothing reads them earlier.
   u32x4 xf[16];
-  {
-    const int m = lane & 15;
-    const uint16_t* xr = X + (int64_t)(m < M ? m : 0) * p.lda + kw + 8 * (lane >> 4);
-#pragma unroll
-    for (int s = 0; s < 16; ++s)
-      xf[s] = m < M ? *reinterpret_cast<const u32x4*>(xr + 32 * s) : u32x4{0u, 0u, 0u, 0u};
-  }
+  const int xm = lane & 15;
+  const uint16_t* xr = X + (int64_t)(xm < M ? xm : 0) * p.lda + kw + 8 * (lane >> 4);
+  auto xload = [&](auto Lc) {
+    constexpr int L = decltype(Lc)::value;
+    xf[2 * L] = gload16_nowait<128 * L>(xr);
+    xf[2 * L + 1] = gload16_nowait<128 * L + 64>(xr);
+  };
+  auto xtie = [&](auto Lc) {
+    constexpr int L = decltype(Lc)::value;
+    tie2(xf[2 * L], xf[2 * L + 1]);
+    if (xm >= M) xf[2 * L] = xf[2 * L + 1] = u32x4{0u, 0u, 0u, 0u};  // rows past M
+  };
+  static_for<R - 1>([&](auto Lc) {
+    issue(0, Lc);
+    xload(Lc);
+  });
 
   // Fragment offsets inside a tile: row l & 15, chunk 4 h + (l >> 4).
   const int f0 = (lane & 15) * 128 + (((lane >> 4) ^ (lane & 7)) << 4);
@@ -207,17 +233,32 @@ __global__ __launch_bounds__(NW * 64) void skinny16l_kernel(GemmParams p) {
         constexpr int LN = (L + R - 1) & 7;
         const int nb = blk + ((L + R - 1) >> 3);
         // The fences keep load issue, waits, LDS reads and MFMAs in program
-        // order: the wait counts below count exactly the loads issued above
-        // (plus the older x loads, which complete first).
+        // order: the wait counts below count exactly the loads issued above.
         __builtin_amdgcn_sched_barrier(0);
         if (nb < nblk) issue(nb, std::integral_constant<int, LN>{});
+        if constexpr (L + R - 1 < 8) {
+          if (blk == 0) xload(std::integral_constant<int, L + R - 1>{});
+        }
         __builtin_amdgcn_sched_barrier(0);
-        // Tiles issued after this one: min(R - 1, T - 1 - t), two loads each.
-        const int after = T - 1 - (blk * 8 + L);
+        // Loads issued after this tile's own: those of the next
+        // min(R - 1, T - 1 - t) tiles, two W loads each plus two x loads
+        // for tiles of the first row block.
+        const int t = blk * 8 + L;
+        const int after = T - 1 - t;
         static_for<R>([&](auto Ac) {
           constexpr int AF = decltype(Ac)::value;
-          if (AF == R - 1 ? after >= AF : after == AF) __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * AF, 63));
+          if (AF == R - 1 ? after >= AF : after == AF) {
+            if (blk == 0) {
+              // tiles t+1 .. t+AF; those below 8 carry x loads
+              constexpr int XL = (L + AF < 8 ? AF : (7 - L > 0 ? 7 - L : 0));
+              __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * AF + 2 * XL, 63));
+            } else {
+              __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * AF, 63));
+            }
+          }
         });
+        __builtin_amdgcn_sched_barrier(0);
+        if (blk == 0) xtie(Lc);
         __builtin_amdgcn_sched_barrier(0);
         const uint32_t a = ring_a + (L % R) * TILE + f0;
         const u32x4 w0 = ds_read16<0>(a);       // chunk l >> 4
