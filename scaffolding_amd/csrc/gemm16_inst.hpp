@@ -8,15 +8,16 @@
 
 namespace sf {
 
-// Row-segment skinny stream: NW = K / 512 waves (K in {2048, 4096, 8192}).
+// Row-segment skinny stream: NW = K / 512 waves (K in {2048, 4096, 8192}),
+// an 8-tile LDS ring per wave where it fits (NW * 16 KB), else 4 tiles.
 template <typename TIn, typename TOut>
 static int launch_skinny_line(const GemmParams& p, const dim3& g, hipStream_t st) {
   switch (p.K) {
     case 2048:
-      hipLaunchKernelGGL((skinny16l_kernel<TIn, TOut, 4>), g, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((skinny16l_kernel<TIn, TOut, 4, 8>), g, dim3(256), 0, st, p);
       return SF_OK;
     case 4096:
-      hipLaunchKernelGGL((skinny16l_kernel<TIn, TOut, 8>), g, dim3(512), 0, st, p);
+      hipLaunchKernelGGL((skinny16l_kernel<TIn, TOut, 8, 8>), g, dim3(512), 0, st, p);
       return SF_OK;
     case 8192:
       hipLaunchKernelGGL((skinny16l_kernel<TIn, TOut, 16>), g, dim3(1024), 0, st, p);
