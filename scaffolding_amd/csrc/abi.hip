@@ -338,6 +338,39 @@ static int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K,
   p.split = 0;
   p.ws = nullptr;
   p.counters = nullptr;
+  if (plan.fp32 && batch == 1 && K >= 128 && (plan.cfg == TILE_128x128 || plan.cfg == TILE_64x64)) {
+    // fp32 with fewer tiles than CUs: split every tile along k (each part at
+    // least 4 slices of 32), on 128 x 128 tiles when that reaches half the
+    // CUs, else on 64 x 64 tiles.
+    const int64_t KT = cdiv(K, 32);
+    auto parts = [&](int64_t t) {
+      int64_t sp = cus / (t > 0 ? t : 1);
+      if (sp > 8) sp = 8;
+      if (sp > KT / 4) sp = KT / 4;
+      return sp < 1 ? (int64_t)1 : sp;
+    };
+    const int64_t t128 = cdiv(M, 128) * cdiv(N, 128), t64 = cdiv(M, 64) * cdiv(N, 64);
+    if (t128 < cus) {
+      const int64_t s128 = parts(t128), s64 = parts(t64);
+      int cfg = -1;
+      int64_t sp = 1;
+      if (s128 >= 2 && 2 * t128 * s128 >= cus) {
+        cfg = TILE_128x128;
+        sp = s128;
+      } else if (t64 < cus && s64 >= 2) {
+        cfg = TILE_64x64;
+        sp = s64;
+      }
+      if (cfg >= 0) {
+        plan.cfg = cfg;
+        tile_dims(plan.cfg, plan.fp32, bm, bn);
+        p.tiles_m = (int)cdiv(M, bm);
+        p.tiles_n = (int)cdiv(N, bn);
+        p.full_tiles = 0;
+        p.split = (int)sp;
+      }
+    }
+  }
   if (plan.cfg == TILE_NT_BIG && batch == 1 && K >= 128) {
     // Tail split: with R = tiles % CUs left over after whole waves, run the
     // last R tiles as R * s workgroups of K / s each (s <= CUs / R), so the
@@ -374,6 +407,15 @@ int sf_gemm(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t bat
                         strideC, ab_dtype, c_dtype, alpha, bias, epi, true, plan);
   if (rc != SF_OK || plan.noop) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (plan.fp32 && plan.p.split > 0) {
+    const int tiles = plan.p.tiles_m * plan.p.tiles_n;
+    const size_t part_bytes = (size_t)(plan.cfg == TILE_128x128 ? 16 : 4) * 256u * 16u;
+    rc = split_workspace_acquire((size_t)tiles * plan.p.split * part_bytes, tiles, st, &plan.p.ws, &plan.p.counters);
+    if (rc != SF_OK) return rc;
+    rc = launch_gemm32(plan.a_kmajor, plan.b_kmajor, plan.cfg, plan.p, batch, st);
+    const int rc2 = split_workspace_release(st);
+    return rc != SF_OK ? rc : rc2;
+  }
   if (plan.fp32) return launch_gemm32(plan.a_kmajor, plan.b_kmajor, plan.cfg, plan.p, batch, st);
   if (plan.p.split > 0) {
     const int nsplit = plan.p.tiles_m * plan.p.tiles_n - plan.p.full_tiles;

@@ -95,30 +95,6 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-// 16-byte global store with the sc0 sc1 cache-policy bits: the agent-scope
-// coherent form the compiler emits for relaxed agent-scope atomic stores
-// (visible across the XCDs' separate L2s once complete), four times wider.
-// Completion is ordered by the caller's s_waitcnt vmcnt(0).
-__device__ __forceinline__ void store16_coherent(float* p, f32x4 v) {
-  asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
-}
-
-// 16-byte coherent global load (sc0 sc1) issued without waiting; the caller
-// must pass the result through wait_vm0_tie8 before using it.
-__device__ __forceinline__ f32x4 load16_coherent_nowait(const float* p) {
-  f32x4 v;
-  asm volatile("global_load_dwordx4 %0, %1, off sc0 sc1" : "=v"(v) : "v"(p) : "memory");
-  return v;
-}
-// s_waitcnt vmcnt(0) that the eight loaded values depend on, so no use of
-// them is scheduled above the wait.
-__device__ __forceinline__ void wait_vm0_tie8(f32x4 (&v)[8]) {
-  asm volatile("s_waitcnt vmcnt(0)"
-               : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7])
-               :
-               : "memory");
-}
-
 // s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] |
 // lgkmcnt[11:8] | vmcnt[5:4] << 14); counts not being waited on are at max.
 constexpr int waitcnt_imm(int vm, int lgkm) {
@@ -370,6 +346,7 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   if (NSTAGE == 2 && part >= 0) {
     const int tid = threadIdx.x;
     float* mine = p.ws + (size_t)(split_tile * p.split + part) * (FN * FM * 512 * 4);
+    mfma_drain();
 #pragma unroll
     for (int i = 0; i < FN; ++i)
 #pragma unroll
@@ -391,19 +368,16 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
       f32x4 sum[FM];
 #pragma unroll
       for (int j = 0; j < FM; ++j) sum[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      // Every part, this one included, is read back from the workspace: one
+      // straight-line loop, the same additions whichever part is last.
       for (int q = 0; q < p.split; ++q) {
-        if (q == part) {
+        const float* src = all + ((size_t)q * (FN * FM) + i * FM) * 512 * 4 + (size_t)tid * 4;
+        f32x4 v[FM];
 #pragma unroll
-          for (int j = 0; j < FM; ++j) sum[j] += acc[i][j];
-        } else {
-          const float* src = all + ((size_t)q * (FN * FM) + i * FM) * 512 * 4 + (size_t)tid * 4;
-          f32x4 v[FM];
+        for (int j = 0; j < FM; ++j) v[j] = load16_coherent_nowait(src + (size_t)j * 512 * 4);
+        wait_vm0_tie8(v);
 #pragma unroll
-          for (int j = 0; j < FM; ++j) v[j] = load16_coherent_nowait(src + (size_t)j * 512 * 4);
-          wait_vm0_tie8(v);
-#pragma unroll
-          for (int j = 0; j < FM; ++j) sum[j] += v[j];
-        }
+        for (int j = 0; j < FM; ++j) sum[j] += v[j];
       }
 #pragma unroll
       for (int j = 0; j < FM; ++j) acc[i][j] = sum[j];

@@ -24,7 +24,8 @@ static int launch32_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hi
 }
 
 int launch_gemm32(bool a_kmajor, bool b_kmajor, int cfg, const GemmParams& p, int64_t batch, hipStream_t st) {
-  const unsigned gx = static_cast<unsigned>(p.tiles_m) * static_cast<unsigned>(p.tiles_n);
+  const unsigned gx = static_cast<unsigned>(p.tiles_m) * static_cast<unsigned>(p.tiles_n) *
+                     static_cast<unsigned>(p.split > 0 ? p.split : 1);
   // grid.y is limited to 65535: walk the batch in chunks.
   for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
     const int64_t nb = (batch - b0) < 65535 ? (batch - b0) : 65535;

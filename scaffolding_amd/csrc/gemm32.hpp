@@ -58,9 +58,13 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm32_kernel(GemmParam
   const int wn = wave % WAVES_N;
   const int g = lane >> 4;
 
+  // Split-K (p.split > 0, batch 1): workgroup x is part x % split of tile
+  // x / split; part q covers k-slices [KT q / split, KT (q + 1) / split).
+  const int part = p.split > 0 ? (int)(blockIdx.x % (unsigned)p.split) : -1;
+  const int tile_id = p.split > 0 ? (int)(blockIdx.x / (unsigned)p.split) : 0;
   int tm, tn;
   {
-    int pid = xcd_remap(blockIdx.x, gridDim.x);
+    int pid = p.split > 0 ? tile_id : xcd_remap(blockIdx.x, gridDim.x);
     group_tile(pid, p.tiles_m, p.tiles_n, 8, tm, tn);
   }
   const int m0 = tm * BM;
@@ -179,18 +183,62 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm32_kernel(GemmParam
     }
   };
 
-  const int KT = (K + BK - 1) / BK;
-  if (KT > 0) {
-    load_tiles(0);
+  const int KTall = (K + BK - 1) / BK;
+  const int kt0 = part >= 0 ? KTall * part / p.split : 0;
+  const int kt1 = part >= 0 ? KTall * (part + 1) / p.split : KTall;
+  if (kt1 > kt0) {
+    load_tiles(kt0 * BK);
     store_tiles(0);
     __syncthreads();
-    for (int kt = 0; kt < KT; ++kt) {
-      const bool more = kt + 1 < KT;
+    for (int kt = kt0; kt < kt1; ++kt) {
+      const bool more = kt + 1 < kt1;
       if (more) load_tiles((kt + 1) * BK);
-      compute(kt & 1);
-      if (more) store_tiles((kt + 1) & 1);
+      compute((kt - kt0) & 1);
+      if (more) store_tiles((kt - kt0 + 1) & 1);
       __syncthreads();
     }
+  }
+
+  // ---- split-K: park the partial, the last part sums all of them in part
+  // order (the same protocol as the 16-bit LDS-DMA kernel's split tail:
+  // coherent stores, a relaxed agent-scope counter, coherent loads).
+  if (part >= 0) {
+    constexpr int NF = FN * FM;
+    float* mine = p.ws + (size_t)(tile_id * p.split + part) * (NF * NT * 4);
+    mfma_drain();
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j) store16_coherent(mine + (size_t)((i * FM + j) * NT + tid) * 4, acc[i][j]);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    __shared__ int arrived;
+    if (tid == 0)
+      arrived = __hip_atomic_fetch_add(&p.counters[tile_id], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (arrived != p.split - 1) return;  // workgroup-uniform
+    const float* all = p.ws + (size_t)tile_id * p.split * (NF * NT * 4);
+    static_assert(NF % 4 == 0, "partials move four fragments at a time");
+#pragma unroll
+    for (int c = 0; c < NF / 4; ++c) {
+      f32x4 sum[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) sum[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      // Every part, this one included, is read back from the workspace: one
+      // straight-line loop, the same additions whichever part is last.
+      for (int q = 0; q < p.split; ++q) {
+        const float* src = all + ((size_t)q * NF + 4 * c) * NT * 4 + (size_t)tid * 4;
+        f32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = load16_coherent_nowait(src + (size_t)u * NT * 4);
+        wait_vm0_tie4(v);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) sum[u] += v[u];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[(4 * c + u) / FM][(4 * c + u) % FM] = sum[u];
+    }
+    if (tid == 0) __hip_atomic_store(&p.counters[tile_id], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
   float* C = static_cast<float*>(p.C) + b * p.sC;

@@ -327,3 +327,38 @@ def test_shape_errors():
         g.dev_matmul(a, up(np.zeros((8, 3), np.float32), "bfloat16"))
     with pytest.raises(ValueError):
         g.dev_linear_forward(a, up(np.zeros((3, 7), np.float32), "float32"))
+
+
+FP32_SPLIT = [
+    # (M, N, K, transB, expected plan)
+    (64, 512, 512, True, "gemm tile 64x64 fp32 split-tail 8x4"),
+    (1024, 1024, 1024, False, "gemm tile 128x128 fp32 split-tail 64x4"),
+    (500, 700, 3000, False, "gemm tile 128x128 fp32 split-tail 24x8"),
+    (300, 260, 1000, True, "gemm tile 64x64 fp32 split-tail 25x8"),
+]
+
+
+@pytest.mark.parametrize("case", FP32_SPLIT, ids=lambda c: "%dx%dx%d-%s" % (c[0], c[1], c[2], "NT" if c[3] else "NN"))
+def test_fp32_split_k(case):
+    """fp32 GEMMs with fewer tiles than CUs split every tile along k; the
+    last part adds the partials in part order: checked elementwise against
+    fp64 and the fp32 CPU path, and bit-identical across two runs."""
+    m, n, k, nt, expect = case
+    rng = np.random.default_rng(m + n + k)
+    a = rnd(rng, (m, k), 1.0, "float32")
+    b = rnd(rng, (n, k) if nt else (k, n), 1.0 / np.sqrt(k), "float32")
+    ga, gb = up(a, "float32"), up(b, "float32")
+    plan = cu().gemm_plan(1 if nt else 0, m, n, k, 1, ga.data_ptr, k, 0, gb.data_ptr, k if nt else n, 0, n, 0,
+                          ga.dtype)
+    assert plan == expect, plan
+    fn = cu().dev_matmul_nt if nt else cu().dev_matmul
+    y1 = fn(ga, gb)
+    y2 = fn(ga, gb)
+    assert np.array_equal(cu().gputensor_to_numpy(y1), cu().gputensor_to_numpy(y2))
+    y = down(y1)
+    bm = (b.T if nt else b).astype(np.float64)
+    y64 = a.astype(np.float64) @ bm
+    absprod = np.abs(a.astype(np.float64)) @ np.abs(bm)
+    check_bound(y, y64, gemm_bound(y64, absprod, k, "float32"), "fp32 split %s" % (case,))
+    y_cpu = ref.matmul_nt(a, b) if nt else ref.matmul(a, b)
+    assert normwise_err(y, y_cpu) <= tol_fp32(k)
