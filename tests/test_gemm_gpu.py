@@ -332,7 +332,8 @@ def test_shape_errors():
 FP32_SPLIT = [
     # (M, N, K, transB, expected plan)
     (64, 512, 512, True, "gemm tile 64x64 fp32 split-tail 8x4"),
-    (1024, 1024, 1024, False, "gemm tile 128x128 fp32 split-tail 64x4"),
+    (768, 768, 1024, False, "gemm tile 128x128 fp32 split-tail 36x7"),
+    (1024, 1024, 1024, False, "gemm tile 64x64 fp32"),
     (500, 700, 3000, False, "gemm tile 128x128 fp32 split-tail 24x8"),
     (300, 260, 1000, True, "gemm tile 64x64 fp32 split-tail 25x8"),
 ]
