@@ -9,7 +9,7 @@ Cython seam ``scaffolding_amd._cuda_ops``.
 The package computes on the GPU only: tensors on the CPU device can be
 created and moved, but the path's operators raise for them, and importing
 the package fails if the native extension has not been built
-(``python -m scaffolding_amd.build``).
+(``python scaffolding_amd/build.py``).
 """
 from . import _cuda_ops as _cuops  # noqa: F401  (fails loudly if not built)
 from .dtype import bfloat16, dtype, float16, float32

@@ -5,7 +5,7 @@
 2. ``_cuda_ops.pyx`` -> C with Cython -> ``_cuda_ops*.so`` with the host C
    compiler, linked against libsfgemm.so through an ``$ORIGIN`` rpath.
 
-Run ``python -m scaffolding_amd.build`` (or ``__graft_entry__.build()``).
+Run ``python scaffolding_amd/build.py`` (or ``__graft_entry__.build()``).
 Artefacts stay in the source tree (git-ignored) so they travel with it.
 """
 from __future__ import annotations

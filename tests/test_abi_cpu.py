@@ -22,7 +22,7 @@ I64 = ctypes.c_int64
 @pytest.fixture(scope="module")
 def lib():
     if not os.path.exists(LIB):
-        pytest.fail("libsfgemm.so not built: run python -m scaffolding_amd.build")
+        pytest.fail("libsfgemm.so not built: run python scaffolding_amd/build.py")
     so = ctypes.CDLL(LIB)
     so.sf_last_error.restype = ctypes.c_char_p
     so.sf_status_string.restype = ctypes.c_char_p
