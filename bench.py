@@ -219,6 +219,37 @@ def sweep(d: Dev, steps: int, warmup: int, only: str | None):
         rec(name, ms, 4.0 * tokens * n * k, (2 * tokens * n + 2 * tokens * k + 2 * n * k) * 2.0, "mfma", PEAK_BF16)
         del x, w, g
 
+    # C5 DiT block glue at the same shape: the fused adaptive layer norm, the
+    # fused attention over the 30 packed heads (17776 x 17776 per head), and
+    # the whole GPU-resident DiTBlock forward (reference
+    # diffusion/models.py:538-590, self-attention + SiLU MLP, cond_dim 512).
+    if want("C5_bf16_ada_layer_norm"):
+        x = d.rand((1, tokens, 1920), 1.0, "bfloat16")
+        prm = d.rand((1, 2 * 1920), 0.1, "bfloat16")
+        gm = d.rand((1920,), 1.0, "bfloat16")
+        bt = d.rand((1920,), 0.1, "bfloat16")
+        ms = d.time_steps(lambda i: cu.dev_ada_layer_norm(x, prm, 1e-5, gm, bt), steps, warmup)
+        rec("C5_bf16_ada_layer_norm", ms, 0.0, 2.0 * tokens * 1920 * 2, "hbm", PEAK_BF16)
+        del x
+    if want("C5_bf16_attention_packed"):
+        qkv = d.rand((1, tokens, 3 * 1920), 1.0, "bfloat16")
+        ms = d.time_steps(lambda i: cu.dev_attention_packed(qkv, 30), max(3, steps // 10), 2)
+        rec("C5_bf16_attention_packed", ms, 4.0 * 30 * tokens * tokens * 64, 4.0 * tokens * 1920 * 2, "mfma",
+            PEAK_BF16)
+        del qkv
+    if want("C5_bf16_dit_block"):
+        import scaffolding_amd as sf
+        from scaffolding_amd.diffusion import DiTBlock
+        dim, heads, cdim = 1920, 30, 512
+        blk = DiTBlock(dim, heads, cdim, dtype="bfloat16")
+        x = sf.Tensor._wrap_gpu(d.rand((1, tokens, dim), 1.0, "bfloat16"))
+        cond = sf.Tensor._wrap_gpu(d.rand((1, cdim), 1.0, "bfloat16"))
+        ms = d.time_steps(lambda i: blk(x, cond)._gpu, max(3, steps // 10), 2)
+        proj = 2.0 * tokens * dim * (3 * dim + dim + 4 * dim + 4 * dim) + 3 * 2.0 * cdim * 2 * dim
+        rec("C5_bf16_dit_block", ms, proj + 4.0 * heads * tokens * tokens * (dim // heads),
+            (tokens * dim * 2 * 11 + 12 * dim * dim) * 2.0, "mfma", PEAK_BF16)
+        del blk, x
+
     # Headline variant with the SiLU epilogue fused.
     if want("north_star_bias_silu"):
         x = d.rand((4096, 4096), 1.0, "bfloat16")

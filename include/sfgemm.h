@@ -97,8 +97,10 @@ int sf_version(void);
  *   C is M x N, ldc >= N.
  *   strideA/B/C: element offset between consecutive batch entries;
  *   strideA or strideB 0 broadcasts that operand over the batch (this is
- *   np.matmul's rule for a 2-D operand); strideC must be >= M*ldc when
- *   batch > 1.
+ *   np.matmul's rule for a 2-D operand); when batch > 1 the entries of C
+ *   must not overlap: strideC >= (M-1)*ldc + N (whole matrices apart), or
+ *   strideC >= N with (batch-1)*strideC + N <= ldc (side by side within
+ *   each row, e.g. attention heads written into [S, heads * D]).
  *
  * Dtypes: ab_dtype in {F32, F16, BF16} for both A and B.  c_dtype is
  * ab_dtype or F32.  bias (length N, NULL unless the epilogue has BIAS) has
@@ -114,6 +116,25 @@ int sf_gemm(int transA, int transB,
             void* C, int64_t ldc, int64_t strideC,
             sf_dtype ab_dtype, sf_dtype c_dtype, float alpha,
             const void* bias, sf_epilogue epi, void* stream);
+
+/* sf_gemm with a residual added after the epilogue, before the single
+ * rounding to c_dtype:
+ *   C[b] = epi(alpha * op(A[b]) . op(B[b]) (+ bias)) + R[b]
+ * R[b] is M x N of dtype c_dtype, row stride ldr >= N, batch stride
+ * strideR (0 broadcasts).  R may be C itself (R == C with ldr == ldc and
+ * strideR == strideC: an in-place residual accumulate); any other overlap
+ * of R and C is undefined.  Replaces the residual adds of the reference's
+ * DiT block, x + self_out(attn) and x + ff(h) (diffusion/models.py:560-564,
+ * :586-589), which run as separate host-side passes there.  Every other
+ * argument, rule and error as sf_gemm; R == NULL is SF_ERR_INVALID_ARG. */
+int sf_gemm_add(int transA, int transB,
+                int64_t M, int64_t N, int64_t K, int64_t batch,
+                const void* A, int64_t lda, int64_t strideA,
+                const void* B, int64_t ldb, int64_t strideB,
+                void* C, int64_t ldc, int64_t strideC,
+                sf_dtype ab_dtype, sf_dtype c_dtype, float alpha,
+                const void* bias, sf_epilogue epi,
+                const void* R, int64_t ldr, int64_t strideR, void* stream);
 
 /* Diagnostic twin of sf_gemm: validates the same arguments and writes the
  * name of the kernel sf_gemm would launch (e.g. "gemm tile 256x256",
@@ -147,15 +168,68 @@ int sf_sum_dim(const void* x, void* out, int64_t outer, int64_t dim_size, int64_
  * memory.  Replaces the three-launch GPU path of
  * scaled_dot_product_attention (nn/functional.py:310-321: dev_batched_matmul_nt,
  * dev_muls, dev_softmax, dev_batched_matmul) when there is no mask and no
- * dropout.  Requires D == 64, Sk % 64 == 0, 16-byte aligned rows
- * (SF_ERR_UNSUPPORTED otherwise: callers fall back to sf_gemm +
- * sf_softmax_rows). */
+ * dropout.  Requires D == 64, 0 < scale < inf, 16-byte aligned rows and
+ * strides (SF_ERR_UNSUPPORTED otherwise: callers fall back to sf_gemm +
+ * sf_softmax_rows).  Any Sk >= 1. */
 int sf_attention(const void* Q, int64_t ldq, int64_t strideQ,
                  const void* K, int64_t ldk, int64_t strideK,
                  const void* V, int64_t ldv, int64_t strideV,
                  void* O, int64_t ldo, int64_t strideO,
                  int64_t batch, int64_t Sq, int64_t Sk, int64_t D,
                  float scale, sf_dtype dtype, void* stream);
+
+/* sf_attention over batch x heads (b, h) pairs, each operand addressed as
+ *   Q + b * strideQ + h * headQ  (rows of ldq), likewise K, V and O.
+ * With a packed projection qkv [batch, S, 3 * heads * 64] this reads Q, K
+ * and V in place (ld = 3 * heads * 64, head stride 64, K and V at column
+ * offsets heads * 64 and 2 * heads * 64) and writes O straight into
+ * [batch, S, heads * 64] (ldo = heads * 64, head stride 64): the head split
+ * qkv[..., i*C:(i+1)*C].reshape(B, N, H, D).transpose(0, 2, 1, 3) and the
+ * merge .transpose(0, 2, 1, 3).reshape(B, N, C) of the reference's DiT
+ * block (diffusion/models.py:551-559, :573-577) cost no copies.  The
+ * output's (b, h) entries must not overlap (heads side by side within a
+ * row, or whole matrices apart).  Rules and errors as sf_attention. */
+int sf_attention_heads(const void* Q, int64_t ldq, int64_t strideQ, int64_t headQ,
+                       const void* K, int64_t ldk, int64_t strideK, int64_t headK,
+                       const void* V, int64_t ldv, int64_t strideV, int64_t headV,
+                       void* O, int64_t ldo, int64_t strideO, int64_t headO,
+                       int64_t batch, int64_t heads, int64_t Sq, int64_t Sk, int64_t D,
+                       float scale, sf_dtype dtype, void* stream);
+
+/* Layer normalisation of `rows` contiguous rows of `cols` elements, with an
+ * optional per-group affine modulation (adaptive layer norm):
+ *   mu = mean(x[r,:]),  var = mean((x[r,:] - mu)^2)  (population variance)
+ *   h  = (x[r,c] - mu) / sqrt(var + eps) * gamma[c] + beta[c]
+ *   y[r,c] = h * (1 + mod_scale[g, c]) + mod_shift[g, c],  g = r / group_rows
+ * gamma / beta: length cols, dtype `dt`, NULL for 1 / 0.  mod_scale /
+ * mod_shift: NULL for none, else rows of `cols` elements of dtype `dt`,
+ * `mod_ld` elements apart (both may point into one [groups, 2 * cols]
+ * projection, shift = scale + cols).  mean_out / rstd_out: NULL, or fp32
+ * arrays of `rows` receiving mu and 1 / sqrt(var + eps).  x, y of dtype
+ * `dt` (F32, F16, BF16); fp32 arithmetic, one rounding per output; x == y
+ * is allowed.
+ * Replaces cuda_layer_norm_f32 (_cuda_kernels.cu:1013-1093, decl
+ * _cuda_ops_decl.h:99-101, the GPU path of
+ * nn.LayerNorm, nn/layers.py:470-493; CPU path :512-521) and, with the
+ * modulation, AdaLayerNorm.forward (diffusion/models.py:479-486: LayerNorm,
+ * then h * (scale + 1) + shift on the host).  Asynchronous on `stream`. */
+int sf_layer_norm(const void* x, void* y, int64_t rows, int64_t cols,
+                  const void* gamma, const void* beta, float eps,
+                  const void* mod_scale, const void* mod_shift, int64_t mod_ld, int64_t group_rows,
+                  float* mean_out, float* rstd_out, sf_dtype dt, void* stream);
+
+/* RMS normalisation: y[r,c] = x[r,c] / sqrt(mean(x[r,:]^2) + eps) * gamma[c]
+ * (gamma NULL for 1), fp32 arithmetic, dtype `dt` in and out, x == y
+ * allowed.  Replaces cuda_rms_norm_f32 (_cuda_kernels.cu:1102-1160, decl
+ * _cuda_ops_decl.h:102; CPU path nn/layers.py:576-581). */
+int sf_rms_norm(const void* x, void* y, int64_t rows, int64_t cols,
+                const void* gamma, float eps, sf_dtype dt, void* stream);
+
+/* y = a + b over n contiguous elements of dtype `dt` (fp32 add, one
+ * rounding); y may equal a or b.  Replaces cuda_add_f32 (decl
+ * _cuda_ops_decl.h:56, dev_add _cuda_ops.pyx:965-966): the residual add where it is not fused into a
+ * GEMM (sf_gemm_add). */
+int sf_add(const void* a, const void* b, void* y, int64_t n, sf_dtype dt, void* stream);
 
 /* Row softmax: y[r,:] = softmax(scale * x[r,:]) for r in [0, rows).
  * Contiguous rows of `cols` elements.  Replaces cuda_softmax_f32

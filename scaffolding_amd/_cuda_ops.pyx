@@ -28,6 +28,7 @@ import numpy as np
 cimport numpy as cnp
 from libc.stdint cimport int64_t, uintptr_t
 from libc.string cimport memset
+from libc.math cimport sqrt
 
 cnp.import_array()
 
@@ -72,6 +73,26 @@ cdef extern from "sfgemm.h" nogil:
                      void* O, int64_t ldo, int64_t strideO,
                      int64_t batch, int64_t Sq, int64_t Sk, int64_t D,
                      float scale, sf_dtype dtype, void* stream)
+    int sf_gemm_add(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t batch,
+                    const void* A, int64_t lda, int64_t strideA,
+                    const void* B, int64_t ldb, int64_t strideB,
+                    void* C, int64_t ldc, int64_t strideC,
+                    sf_dtype ab_dtype, sf_dtype c_dtype, float alpha,
+                    const void* bias, sf_epilogue epi,
+                    const void* R, int64_t ldr, int64_t strideR, void* stream)
+    int sf_attention_heads(const void* Q, int64_t ldq, int64_t strideQ, int64_t headQ,
+                           const void* K, int64_t ldk, int64_t strideK, int64_t headK,
+                           const void* V, int64_t ldv, int64_t strideV, int64_t headV,
+                           void* O, int64_t ldo, int64_t strideO, int64_t headO,
+                           int64_t batch, int64_t heads, int64_t Sq, int64_t Sk, int64_t D,
+                           float scale, sf_dtype dtype, void* stream)
+    int sf_layer_norm(const void* x, void* y, int64_t rows, int64_t cols,
+                      const void* gamma, const void* beta, float eps,
+                      const void* mod_scale, const void* mod_shift, int64_t mod_ld, int64_t group_rows,
+                      float* mean_out, float* rstd_out, sf_dtype dt, void* stream)
+    int sf_rms_norm(const void* x, void* y, int64_t rows, int64_t cols,
+                    const void* gamma, float eps, sf_dtype dt, void* stream)
+    int sf_add(const void* a, const void* b, void* y, int64_t n, sf_dtype dt, void* stream)
     int sf_softmax_rows(const void* x, void* y, int64_t rows, int64_t cols,
                         sf_dtype in_dtype, sf_dtype out_dtype, float scale, void* stream)
     int sf_silu(const void* x, void* y, int64_t n, sf_dtype dt, void* stream)
@@ -390,6 +411,17 @@ def gputensor_to_device(gt, int target_dev):
     return out
 
 
+def dev_copy(gt_src, gt_dst):
+    """Copies src's bytes into dst on the device (reference :1354-1364):
+    equal element counts and dtypes, asynchronous on the default stream."""
+    if gt_src.numel != gt_dst.numel or gt_src.dtype != gt_dst.dtype:
+        raise ValueError("dev_copy: %s %s into %s %s" % (gt_src.shape, gt_src.dtype, gt_dst.shape, gt_dst.dtype))
+    if gt_src.numel == 0:
+        return gt_dst
+    _check_cuda(sf_memcpy_d2d(_ptr(gt_dst), _ptr(gt_src), <size_t>gt_src.nbytes, NULL))
+    return gt_dst
+
+
 def dev_cast(gt, dtype):
     """Device dtype conversion (RNE)."""
     dt = resolve_dtype(dtype)
@@ -553,7 +585,7 @@ cdef object _same_dtype(a, b, str name):
 
 cdef object _gemm(int transB, int64_t M, int64_t N, int64_t K, int64_t batch,
                   a, int64_t strideA, b, int64_t ldb, int64_t strideB,
-                  tuple out_shape, float alpha, bias, int epi):
+                  tuple out_shape, float alpha, bias, int epi, residual=None):
     dt = a.dtype
     cdef sf_dtype sdt = _sf_dtype(dt)
     cdef int dev = a.device_id
@@ -562,15 +594,22 @@ cdef object _gemm(int transB, int64_t M, int64_t N, int64_t K, int64_t batch,
     cdef void* pb = _ptr(b)
     cdef void* pc = _ptr(out)
     cdef void* pbias = NULL
+    cdef void* pr = NULL
     if bias is not None:
         pbias = _ptr(bias)
+    if residual is not None:
+        pr = _ptr(residual)
     cdef int ret
     cdef int64_t lda = K if K > 0 else 1
     if transB and ldb < 1:
         ldb = 1
     with nogil:
-        ret = sf_gemm(0, transB, M, N, K, batch, pa, lda, strideA, pb, ldb, strideB,
-                      pc, N, M * N, sdt, sdt, alpha, pbias, <sf_epilogue>epi, NULL)
+        if pr != NULL:
+            ret = sf_gemm_add(0, transB, M, N, K, batch, pa, lda, strideA, pb, ldb, strideB,
+                              pc, N, M * N, sdt, sdt, alpha, pbias, <sf_epilogue>epi, pr, N, M * N, NULL)
+        else:
+            ret = sf_gemm(0, transB, M, N, K, batch, pa, lda, strideA, pb, ldb, strideB,
+                          pc, N, M * N, sdt, sdt, alpha, pbias, <sf_epilogue>epi, NULL)
     _check_kernel(ret)
     return out
 
@@ -784,10 +823,11 @@ def dev_linear_backward(gt_grad, gt_x, gt_weight, bint has_bias=True):
 _ACTS = {None: 0, 'none': 0, 'silu': 1, 'gelu': 2, 'gelu_tanh': 2}
 
 
-def dev_linear_forward(gt_x, gt_weight, gt_bias=None, activation=None):
-    """y = act(x @ W^T + b), one fused launch  (reference :1278-1302, which
-    runs SGEMM then a bias pass; SiLU/GELU were further passes).
-    x (..., K), W (N, K), b (N,) -> y (..., N)."""
+def dev_linear_forward(gt_x, gt_weight, gt_bias=None, activation=None, residual=None):
+    """y = act(x @ W^T + b) (+ residual), one fused launch  (reference
+    :1278-1302, which runs SGEMM then a bias pass; SiLU/GELU and the DiT
+    block's residual adds, diffusion/models.py:563,588, were further passes).
+    x (..., K), W (N, K), b (N,), residual (..., N) -> y (..., N)."""
     _same_dtype(gt_x, gt_weight, 'dev_linear_forward')
     if len(gt_x.shape) < 1 or len(gt_weight.shape) != 2:
         raise ValueError("dev_linear_forward: x must be (..., K) and W (N, K)")
@@ -811,7 +851,14 @@ def dev_linear_forward(gt_x, gt_weight, gt_bias=None, activation=None):
     else:
         epi = (SF_EPI_NONE, SF_EPI_SILU, SF_EPI_GELU_TANH)[act]
     out_shape = tuple(gt_x.shape[:-1]) + (N,)
-    return _gemm(1, M, N, K, 1, gt_x, 0, gt_weight, K, 0, out_shape, 1.0, gt_bias, epi)
+    if residual is not None:
+        if residual.dtype != gt_x.dtype or tuple(residual.shape) != out_shape:
+            raise ValueError("dev_linear_forward: residual must be %s of the input dtype, got %s"
+                             % (out_shape, tuple(residual.shape)))
+        if residual.device_id != gt_x.device_id:
+            raise ValueError("dev_linear_forward: residual on device %d, x on %d"
+                             % (residual.device_id, gt_x.device_id))
+    return _gemm(1, M, N, K, 1, gt_x, 0, gt_weight, K, 0, out_shape, 1.0, gt_bias, epi, residual)
 
 
 def dev_bias_add(gt_c, gt_bias):
@@ -820,6 +867,204 @@ def dev_bias_add(gt_c, gt_bias):
     cdef int64_t M = gt_c.numel // N
     _check_kernel(sf_bias_add_rows(_ptr(gt_c), _ptr(gt_bias), M, N, _sf_dtype(gt_c.dtype), NULL))
     return gt_c
+
+
+# ================================================================
+#  Normalisation and residual glue (reference :965-966, :1195-1241;
+#  diffusion/models.py:470-590)
+# ================================================================
+
+cdef object _need_vector(gt, int64_t n, str name):
+    if gt is None:
+        return None
+    if gt.numel != n:
+        raise ValueError("%s: expected %d elements, got shape %s" % (name, n, gt.shape))
+    return gt
+
+
+def dev_layer_norm(gt_x, gt_gamma=None, gt_beta=None, float eps=1e-5):
+    """Layer norm over the last dim (reference :1195-1216, which takes
+    (N, D) fp32; any rank and the 16-bit dtypes here, result in the input
+    dtype).  gamma / beta: (D,) of the input dtype or None."""
+    if len(gt_x.shape) < 1:
+        raise ValueError("dev_layer_norm: scalar input")
+    cdef int64_t D = gt_x.shape[-1]
+    cdef int64_t rows = gt_x.numel // D if D > 0 else 0
+    for g in (gt_gamma, gt_beta):
+        if g is not None:
+            _same_dtype(gt_x, g, 'dev_layer_norm')
+    _need_vector(gt_gamma, D, 'dev_layer_norm gamma')
+    _need_vector(gt_beta, D, 'dev_layer_norm beta')
+    out = _alloc_like(tuple(gt_x.shape), gt_x.dtype, gt_x.device_id)
+    cdef void* pg = _ptr(gt_gamma) if gt_gamma is not None else NULL
+    cdef void* pb = _ptr(gt_beta) if gt_beta is not None else NULL
+    cdef void* px = _ptr(gt_x)
+    cdef void* py = _ptr(out)
+    cdef sf_dtype dt = _sf_dtype(gt_x.dtype)
+    cdef int ret
+    with nogil:
+        ret = sf_layer_norm(px, py, rows, D, pg, pb, eps, NULL, NULL, 0, 1, NULL, NULL, dt, NULL)
+    _check_kernel(ret)
+    return out
+
+
+def dev_ada_layer_norm(gt_x, gt_params, float eps=1e-5, gt_gamma=None, gt_beta=None):
+    """Adaptive layer norm in one launch (reference AdaLayerNorm.forward,
+    diffusion/models.py:478-486): h = LayerNorm(x) (gamma, beta), then
+    h * (1 + scale) + shift with scale = params[..., :C], shift =
+    params[..., C:].  x (B, N, C) or (N, C); params (B, 2C), (B, 1, 2C) or
+    (2C,): one row of modulation per batch entry, broadcast over its N
+    tokens (the reference's NumPy broadcast does this for B == 1 and for
+    params of shape (B, 1, 2C))."""
+    shape = tuple(gt_x.shape)
+    if len(shape) < 2:
+        raise ValueError("dev_ada_layer_norm: x must be (N, C) or (B, N, C)")
+    cdef int64_t C = shape[-1]
+    cdef int64_t Nt = shape[-2]
+    cdef int64_t B = gt_x.numel // (Nt * C) if Nt * C > 0 else 0
+    _same_dtype(gt_x, gt_params, 'dev_ada_layer_norm')
+    if gt_params.numel != B * 2 * C or gt_params.shape[-1] != 2 * C:
+        raise ValueError("dev_ada_layer_norm: params %s do not hold one (2C,) row per batch entry of x %s"
+                         % (gt_params.shape, shape))
+    for g in (gt_gamma, gt_beta):
+        if g is not None:
+            _same_dtype(gt_x, g, 'dev_ada_layer_norm')
+    _need_vector(gt_gamma, C, 'dev_ada_layer_norm gamma')
+    _need_vector(gt_beta, C, 'dev_ada_layer_norm beta')
+    out = _alloc_like(shape, gt_x.dtype, gt_x.device_id)
+    cdef int64_t rows = B * Nt
+    cdef void* pg = _ptr(gt_gamma) if gt_gamma is not None else NULL
+    cdef void* pb = _ptr(gt_beta) if gt_beta is not None else NULL
+    cdef void* px = _ptr(gt_x)
+    cdef void* py = _ptr(out)
+    cdef char* pm = <char*>_ptr(gt_params)
+    cdef sf_dtype dt = _sf_dtype(gt_x.dtype)
+    cdef void* pshift = pm + C * _itemsize(gt_x.dtype)
+    cdef int ret
+    with nogil:
+        ret = sf_layer_norm(px, py, rows, C, pg, pb, eps, pm, pshift, 2 * C, Nt, NULL, NULL, dt, NULL)
+    _check_kernel(ret)
+    return out
+
+
+def dev_rms_norm(gt_x, gt_gamma=None, float eps=1e-5):
+    """RMS norm over the last dim (reference :1221-1241)."""
+    if len(gt_x.shape) < 1:
+        raise ValueError("dev_rms_norm: scalar input")
+    cdef int64_t D = gt_x.shape[-1]
+    cdef int64_t rows = gt_x.numel // D if D > 0 else 0
+    if gt_gamma is not None:
+        _same_dtype(gt_x, gt_gamma, 'dev_rms_norm')
+    _need_vector(gt_gamma, D, 'dev_rms_norm gamma')
+    out = _alloc_like(tuple(gt_x.shape), gt_x.dtype, gt_x.device_id)
+    cdef void* pg = _ptr(gt_gamma) if gt_gamma is not None else NULL
+    cdef void* px = _ptr(gt_x)
+    cdef void* py = _ptr(out)
+    cdef sf_dtype dt = _sf_dtype(gt_x.dtype)
+    cdef int ret
+    with nogil:
+        ret = sf_rms_norm(px, py, rows, D, pg, eps, dt, NULL)
+    _check_kernel(ret)
+    return out
+
+
+def dev_add(gt_a, gt_b):
+    """a + b elementwise, equal shapes (reference :965-966)."""
+    _same_dtype(gt_a, gt_b, 'dev_add')
+    if tuple(gt_a.shape) != tuple(gt_b.shape):
+        raise ValueError("dev_add: shapes %s and %s differ" % (gt_a.shape, gt_b.shape))
+    out = _alloc_like(tuple(gt_a.shape), gt_a.dtype, gt_a.device_id)
+    cdef void* pa = _ptr(gt_a)
+    cdef void* pb = _ptr(gt_b)
+    cdef void* py = _ptr(out)
+    cdef int64_t n = gt_a.numel
+    cdef sf_dtype dt = _sf_dtype(gt_a.dtype)
+    cdef int ret
+    with nogil:
+        ret = sf_add(pa, pb, py, n, dt, NULL)
+    _check_kernel(ret)
+    return out
+
+
+cdef object _mha_strided(q, int64_t q_off, int64_t ldq, k, int64_t k_off, int64_t ldk,
+                         v, int64_t v_off, int64_t ldv, int64_t B, int64_t Nq, int64_t Sk,
+                         int64_t H, int64_t D, float scale):
+    """Attention of H heads read in place from row-major [B, S, ld] operands
+    (head h at column offset off + h * D), output [B, Nq, H * D]."""
+    dt = q.dtype
+    cdef sf_dtype sdt = _sf_dtype(dt)
+    cdef int64_t C = H * D
+    out = _alloc_like((B, Nq, C), dt, q.device_id)
+    cdef int64_t es = _itemsize(dt)
+    cdef char* pq = <char*>_ptr(q) + q_off * es
+    cdef char* pk = <char*>_ptr(k) + k_off * es
+    cdef char* pv = <char*>_ptr(v) + v_off * es
+    cdef char* po = <char*>_ptr(out)
+    cdef int ret = SF_ERR_UNSUPPORTED
+    if sdt != SF_F32 and D == 64 and scale > 0:
+        with nogil:
+            ret = sf_attention_heads(pq, ldq, Nq * ldq, D, pk, ldk, Sk * ldk, D, pv, ldv, Sk * ldv, D,
+                                     po, C, Nq * C, D, B, H, Nq, Sk, D, scale, sdt, NULL)
+        if ret != SF_ERR_UNSUPPORTED:
+            _check_kernel(ret)
+            return out
+    # Any head size, dtype or scale: per batch entry, scores of all heads by
+    # one strided-batched NT GEMM (the scale in its epilogue), the row
+    # softmax, then one strided-batched NN GEMM writing the heads side by
+    # side into the output rows.
+    scores = _alloc_like((H, Nq, Sk), dt, q.device_id)
+    cdef char* ps = <char*>_ptr(scores)
+    cdef int64_t b
+    for b in range(B):
+        with nogil:
+            ret = sf_gemm(0, 1, Nq, Sk, D, H, pq + b * Nq * ldq * es, ldq, D, pk + b * Sk * ldk * es, ldk, D,
+                          ps, Sk, Nq * Sk, sdt, sdt, scale, NULL, SF_EPI_NONE, NULL)
+        _check_kernel(ret)
+        with nogil:
+            ret = sf_softmax_rows(ps, ps, H * Nq, Sk, sdt, sdt, 1.0, NULL)
+        _check_kernel(ret)
+        with nogil:
+            ret = sf_gemm(0, 0, Nq, D, Sk, H, ps, Sk, Nq * Sk, pv + b * Sk * ldv * es, ldv, D,
+                          po + b * Nq * C * es, C, D, sdt, sdt, 1.0, NULL, SF_EPI_NONE, NULL)
+        _check_kernel(ret)
+    return out
+
+
+def dev_attention_packed(gt_qkv, int heads, scale=None):
+    """Self-attention straight from a packed projection: qkv (B, N, 3C) ->
+    (B, N, C), C = heads * D, q / k / v = qkv[..., 0:C], [C:2C], [2C:3C],
+    head h at columns h*D..h*D+D-1 of each (reference DiTBlock,
+    diffusion/models.py:550-559: head split, _attn, merge).  No split or
+    merge copies: the fused kernel reads the heads in place and writes the
+    merged rows."""
+    shape = tuple(gt_qkv.shape)
+    if len(shape) not in (2, 3) or shape[-1] % (3 * heads) != 0 or heads < 1:
+        raise ValueError("dev_attention_packed: qkv must be (B, N, 3 * heads * D), got %s for %d heads"
+                         % (shape, heads))
+    cdef int64_t B = shape[0] if len(shape) == 3 else 1
+    cdef int64_t N = shape[-2]
+    cdef int64_t C = shape[-1] // 3
+    cdef int64_t D = C // heads
+    s = (1.0 / sqrt(<double>D)) if scale is None else float(scale)
+    out = _mha_strided(gt_qkv, 0, 3 * C, gt_qkv, C, 3 * C, gt_qkv, 2 * C, 3 * C, B, N, N, heads, D, s)
+    return out if len(shape) == 3 else dev_reshape(out, (N, C))
+
+
+def dev_multihead_attention(gt_q, gt_k, gt_v, int heads, scale=None):
+    """Attention over heads packed in the last dim: q (B, N, C), k and v
+    (B, S, C) -> (B, N, C), C = heads * D (the reference's cross-attention,
+    diffusion/models.py:566-577, without its split / merge copies)."""
+    _same_dtype(gt_q, gt_k, 'dev_multihead_attention')
+    _same_dtype(gt_q, gt_v, 'dev_multihead_attention')
+    qs, ks, vs = tuple(gt_q.shape), tuple(gt_k.shape), tuple(gt_v.shape)
+    if len(qs) != 3 or ks != vs or len(ks) != 3 or ks[0] != qs[0] or ks[2] != qs[2] or heads < 1 \
+            or qs[2] % heads != 0:
+        raise ValueError("dev_multihead_attention: q (B, N, C), k and v (B, S, C), C divisible by heads; "
+                         "got %s %s %s" % (qs, ks, vs))
+    cdef int64_t C = qs[2]
+    cdef int64_t D = C // heads
+    s = (1.0 / sqrt(<double>D)) if scale is None else float(scale)
+    return _mha_strided(gt_q, 0, C, gt_k, 0, C, gt_v, 0, C, qs[0], qs[1], ks[1], heads, D, s)
 
 
 # ================================================================
@@ -869,7 +1114,7 @@ def dev_sdpa_unfused(q, k, v, scale=None):
     into its epilogue, row softmax, PV), scores kept in the input dtype:
     the reference GPU path's structure (nn/functional.py:310-321)."""
     d = q.shape[-1]
-    s = (1.0 / float(d) ** 0.5) if scale is None else float(scale)
+    s = (1.0 / sqrt(<double>d)) if scale is None else float(scale)
     scores = dev_batched_matmul_nt(q, k, s)
     probs = dev_softmax(scores, -1)
     del scores
@@ -880,9 +1125,9 @@ def dev_scaled_dot_product_attention(q, k, v, scale=None):
     """softmax(scale * Q K^T) V  (reference GPU path nn/functional.py:310-321).
     q (..., Sq, D), k and v (..., Sk, D) with equal leading dims.  One fused
     launch (sf_attention: scores never reach memory) for 16-bit inputs with
-    D == 64 and Sk % 64 == 0; otherwise the three-launch path."""
+    D == 64 and a positive finite scale; otherwise the three-launch path."""
     d = q.shape[-1]
-    s = (1.0 / float(d) ** 0.5) if scale is None else float(scale)
+    s = (1.0 / sqrt(<double>d)) if scale is None else float(scale)
     _same_dtype(q, k, 'dev_scaled_dot_product_attention')
     _same_dtype(q, v, 'dev_scaled_dot_product_attention')
     if len(q.shape) < 2 or len(k.shape) != len(q.shape) or len(v.shape) != len(q.shape):
@@ -896,7 +1141,7 @@ def dev_scaled_dot_product_attention(q, k, v, scale=None):
     cdef int64_t batch = 1
     for e in q.shape[:-2]:
         batch *= e
-    if q.dtype == np.float32 or d != 64 or sk % 64 != 0:
+    if q.dtype == np.float32 or d != 64 or not (0.0 < s < 3.0e38):
         return dev_sdpa_unfused(q, k, v, scale)
     out = _alloc_like(tuple(q.shape), q.dtype, q.device_id)
     cdef int ret

@@ -82,6 +82,7 @@ int launch_gemm16(sf_dtype in, sf_dtype out, bool a_kmajor, bool b_kmajor, int c
     q.A = static_cast<const uint16_t*>(p.A) + b0 * p.sA;
     q.B = static_cast<const uint16_t*>(p.B) + b0 * p.sB;
     q.C = static_cast<uint8_t*>(p.C) + b0 * p.sC * (out == SF_F32 ? 4 : 2);
+    if (p.res != nullptr) q.res = static_cast<const uint8_t*>(p.res) + b0 * p.sR * (out == SF_F32 ? 4 : 2);
     const int rc = (in == SF_BF16)
                        ? launch_gemm16_bf16(out, a_kmajor, b_kmajor, cfg, q, gx, static_cast<unsigned>(nb), st)
                        : launch_gemm16_f16(out, a_kmajor, b_kmajor, cfg, q, gx, static_cast<unsigned>(nb), st);
@@ -256,7 +257,7 @@ static int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K,
                         const void* A, int64_t lda, int64_t strideA, const void* B, int64_t ldb,
                         int64_t strideB, void* C, int64_t ldc, int64_t strideC, sf_dtype ab_dtype,
                         sf_dtype c_dtype, float alpha, const void* bias, sf_epilogue epi,
-                        bool need_c, GemmPlan& plan) {
+                        const void* R, int64_t ldr, int64_t strideR, bool need_c, GemmPlan& plan) {
   g_err[0] = 0;
   plan.noop = false;
   if (!valid_dtype(ab_dtype) || !valid_dtype(c_dtype))
@@ -293,9 +294,19 @@ static int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K,
                 (long long)K, transA, transB);
   if (strideA < 0 || strideB < 0 || strideC < 0)
     return fail(SF_ERR_INVALID_ARG, "sf_gemm: negative batch stride");
-  if (batch > 1 && strideC < (M - 1) * ldc + N)
-    return fail(SF_ERR_INVALID_ARG, "sf_gemm: strideC=%lld overlaps batch entries (need >= %lld)",
-                (long long)strideC, (long long)((M - 1) * ldc + N));
+  // Batch entries of C must not overlap: whole matrices apart, or side by
+  // side within each row (e.g. attention heads written into [S, heads * D]).
+  if (batch > 1 && strideC < (M - 1) * ldc + N && !(strideC >= N && (batch - 1) * strideC + N <= ldc))
+    return fail(SF_ERR_INVALID_ARG, "sf_gemm: strideC=%lld overlaps batch entries (need >= %lld, or "
+                "side by side within rows of ldc)", (long long)strideC, (long long)((M - 1) * ldc + N));
+  if (R != nullptr) {
+    if (ldr < N || strideR < 0)
+      return fail(SF_ERR_INVALID_ARG, "sf_gemm_add: residual ldr=%lld / strideR=%lld invalid for N=%lld",
+                  (long long)ldr, (long long)strideR, (long long)N);
+    if (R == C && (ldr != ldc || strideR != strideC))
+      return fail(SF_ERR_INVALID_ARG, "sf_gemm_add: an in-place residual (R == C) needs ldr == ldc and "
+                  "strideR == strideC");
+  }
 
   GemmParams& p = plan.p;
   p.A = A; p.B = B; p.C = C; p.bias = bias;
@@ -304,6 +315,9 @@ static int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K,
   p.M = (int)M; p.N = (int)N; p.K = (int)K;
   p.alpha = alpha;
   p.epi = (int)epi;
+  p.res = R;
+  p.ldr = ldr;
+  p.sR = strideR;
   plan.a_kmajor = a_kmajor;
   plan.b_kmajor = b_kmajor;
   const int cus = cu_count_current();
@@ -401,13 +415,14 @@ static int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K,
   return SF_OK;
 }
 
-int sf_gemm(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t batch, const void* A,
-            int64_t lda, int64_t strideA, const void* B, int64_t ldb, int64_t strideB, void* C,
-            int64_t ldc, int64_t strideC, sf_dtype ab_dtype, sf_dtype c_dtype, float alpha,
-            const void* bias, sf_epilogue epi, void* stream) {
+static int gemm_run(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t batch, const void* A,
+                    int64_t lda, int64_t strideA, const void* B, int64_t ldb, int64_t strideB, void* C,
+                    int64_t ldc, int64_t strideC, sf_dtype ab_dtype, sf_dtype c_dtype, float alpha,
+                    const void* bias, sf_epilogue epi, const void* R, int64_t ldr, int64_t strideR,
+                    void* stream) {
   GemmPlan plan;
   int rc = gemm_prepare(transA, transB, M, N, K, batch, A, lda, strideA, B, ldb, strideB, C, ldc,
-                        strideC, ab_dtype, c_dtype, alpha, bias, epi, true, plan);
+                        strideC, ab_dtype, c_dtype, alpha, bias, epi, R, ldr, strideR, true, plan);
   if (rc != SF_OK || plan.noop) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (plan.fp32 && plan.p.split > 0) {
@@ -432,6 +447,27 @@ int sf_gemm(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t bat
   return launch_gemm16(ab_dtype, c_dtype, plan.a_kmajor, plan.b_kmajor, plan.cfg, plan.p, batch, st);
 }
 
+int sf_gemm(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t batch, const void* A,
+            int64_t lda, int64_t strideA, const void* B, int64_t ldb, int64_t strideB, void* C,
+            int64_t ldc, int64_t strideC, sf_dtype ab_dtype, sf_dtype c_dtype, float alpha,
+            const void* bias, sf_epilogue epi, void* stream) {
+  return gemm_run(transA, transB, M, N, K, batch, A, lda, strideA, B, ldb, strideB, C, ldc, strideC, ab_dtype,
+                  c_dtype, alpha, bias, epi, nullptr, 0, 0, stream);
+}
+
+int sf_gemm_add(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t batch, const void* A,
+                int64_t lda, int64_t strideA, const void* B, int64_t ldb, int64_t strideB, void* C,
+                int64_t ldc, int64_t strideC, sf_dtype ab_dtype, sf_dtype c_dtype, float alpha,
+                const void* bias, sf_epilogue epi, const void* R, int64_t ldr, int64_t strideR,
+                void* stream) {
+  if (R == nullptr && M > 0 && N > 0 && batch > 0) {
+    g_err[0] = 0;
+    return fail(SF_ERR_INVALID_ARG, "sf_gemm_add: null residual pointer");
+  }
+  return gemm_run(transA, transB, M, N, K, batch, A, lda, strideA, B, ldb, strideB, C, ldc, strideC, ab_dtype,
+                  c_dtype, alpha, bias, epi, R, ldr, strideR, stream);
+}
+
 int sf_gemm_plan(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t batch,
                  const void* A, int64_t lda, int64_t strideA, const void* B, int64_t ldb,
                  int64_t strideB, void* C, int64_t ldc, int64_t strideC, sf_dtype ab_dtype,
@@ -441,7 +477,7 @@ int sf_gemm_plan(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
   buf[0] = 0;
   GemmPlan plan;
   int rc = gemm_prepare(transA, transB, M, N, K, batch, A, lda, strideA, B, ldb, strideB, C, ldc,
-                        strideC, ab_dtype, c_dtype, alpha, bias, epi, false, plan);
+                        strideC, ab_dtype, c_dtype, alpha, bias, epi, nullptr, 0, 0, false, plan);
   if (rc != SF_OK) return rc;
   char extra[48] = "";
   if (!plan.noop && plan.p.split > 0)
@@ -455,34 +491,120 @@ int sf_gemm_plan(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
   return SF_OK;
 }
 
-int sf_attention(const void* Q, int64_t ldq, int64_t strideQ, const void* K, int64_t ldk, int64_t strideK,
-                 const void* V, int64_t ldv, int64_t strideV, void* O, int64_t ldo, int64_t strideO,
-                 int64_t batch, int64_t Sq, int64_t Sk, int64_t D, float scale, sf_dtype dtype, void* stream) {
+// (b, h) entries of one operand do not overlap: heads side by side within
+// a row (hS >= D, (H-1) hS + D <= ld) or stacked as whole matrices
+// (hS >= (S-1) ld + D), and batch entries past every head's last element.
+static bool attn_out_disjoint(int64_t S, int64_t ld, int64_t sB, int64_t sH, int64_t B, int64_t H, int64_t D) {
+  const int64_t mat = (S - 1) * ld + D;
+  int64_t span;
+  if (H <= 1)
+    span = mat;
+  else if (sH >= D && (H - 1) * sH + D <= ld)
+    span = mat + (H - 1) * sH;
+  else if (sH >= mat)
+    span = (H - 1) * sH + mat;
+  else
+    return false;
+  return B <= 1 || sB >= span;
+}
+
+int sf_attention_heads(const void* Q, int64_t ldq, int64_t strideQ, int64_t headQ, const void* K, int64_t ldk,
+                       int64_t strideK, int64_t headK, const void* V, int64_t ldv, int64_t strideV, int64_t headV,
+                       void* O, int64_t ldo, int64_t strideO, int64_t headO, int64_t batch, int64_t heads,
+                       int64_t Sq, int64_t Sk, int64_t D, float scale, sf_dtype dtype, void* stream) {
   g_err[0] = 0;
   if (!valid_dtype(dtype)) return fail(SF_ERR_INVALID_ARG, "sf_attention: unknown dtype %d", (int)dtype);
-  if (batch < 0 || Sq < 0 || Sk < 0 || D < 0)
+  if (batch < 0 || heads < 0 || Sq < 0 || Sk < 0 || D < 0)
     return fail(SF_ERR_INVALID_ARG, "sf_attention: negative size");
   if (dtype == SF_F32) return fail(SF_ERR_UNSUPPORTED, "sf_attention: 16-bit dtypes only");
   if (D != 64) return fail(SF_ERR_UNSUPPORTED, "sf_attention: head size %lld (64 only)", (long long)D);
-  if (Sk % 64 != 0)
-    return fail(SF_ERR_UNSUPPORTED, "sf_attention: Sk=%lld is not a multiple of 64", (long long)Sk);
-  if (batch == 0 || Sq == 0) return SF_OK;
+  if (!(scale > 0.0f) || scale > 3.0e38f)
+    return fail(SF_ERR_UNSUPPORTED, "sf_attention: scale %g (positive and finite only)", (double)scale);
+  if (batch == 0 || heads == 0 || Sq == 0) return SF_OK;
   if (Sk == 0) return fail(SF_ERR_INVALID_ARG, "sf_attention: softmax over zero keys");
   if (Q == nullptr || K == nullptr || V == nullptr || O == nullptr)
     return fail(SF_ERR_INVALID_ARG, "sf_attention: null pointer");
   if (ldq < D || ldk < D || ldv < D || ldo < D)
     return fail(SF_ERR_INVALID_ARG, "sf_attention: row stride below the head size");
-  if (strideQ < 0 || strideK < 0 || strideV < 0 || strideO < 0)
-    return fail(SF_ERR_INVALID_ARG, "sf_attention: negative batch stride");
-  if (batch > 1 && strideO < (Sq - 1) * ldo + D)
-    return fail(SF_ERR_INVALID_ARG, "sf_attention: strideO overlaps batch entries");
-  if (Sq > INT32_MAX || Sk * (ldk > ldv ? ldk : ldv) * 2 >= (int64_t(1) << 31))
+  if (strideQ < 0 || strideK < 0 || strideV < 0 || strideO < 0 || headQ < 0 || headK < 0 || headV < 0 ||
+      headO < 0)
+    return fail(SF_ERR_INVALID_ARG, "sf_attention: negative batch or head stride");
+  if (!attn_out_disjoint(Sq, ldo, strideO, headO, batch, heads, D))
+    return fail(SF_ERR_INVALID_ARG, "sf_attention: output (batch, head) entries overlap");
+  // Key rows up to the next multiple of 64 past Sk are addressed (and read
+  // as zeros) with 32-bit offsets.
+  if (Sq > INT32_MAX || heads > INT32_MAX || (Sk + 64) * (ldk > ldv ? ldk : ldv) * 2 >= (int64_t(1) << 31))
     return fail(SF_ERR_UNSUPPORTED, "sf_attention: K/V of one batch entry must stay below 2 GiB");
   if (!al16(Q) || !al16(K) || !al16(V) || !al16(O) || ldq % 8 || ldk % 8 || ldv % 8 || ldo % 8 ||
-      strideQ % 8 || strideK % 8 || strideV % 8 || strideO % 8)
+      strideQ % 8 || strideK % 8 || strideV % 8 || strideO % 8 || headQ % 8 || headK % 8 || headV % 8 ||
+      headO % 8)
     return fail(SF_ERR_UNSUPPORTED, "sf_attention: rows must be 16-byte aligned");
-  return launch_attention(Q, K, V, O, batch, Sq, Sk, strideQ, strideK, strideV, strideO, ldq, ldk, ldv, ldo,
-                          scale, dtype, static_cast<hipStream_t>(stream));
+  AttnShape a;
+  a.Q = Q; a.K = K; a.V = V; a.O = O;
+  a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.ldo = ldo;
+  a.sQ = strideQ; a.sK = strideK; a.sV = strideV; a.sO = strideO;
+  a.hQ = headQ; a.hK = headK; a.hV = headV; a.hO = headO;
+  a.batch = batch; a.heads = heads; a.Sq = Sq; a.Sk = Sk;
+  return launch_attention(a, scale, dtype, static_cast<hipStream_t>(stream));
+}
+
+int sf_attention(const void* Q, int64_t ldq, int64_t strideQ, const void* K, int64_t ldk, int64_t strideK,
+                 const void* V, int64_t ldv, int64_t strideV, void* O, int64_t ldo, int64_t strideO,
+                 int64_t batch, int64_t Sq, int64_t Sk, int64_t D, float scale, sf_dtype dtype, void* stream) {
+  return sf_attention_heads(Q, ldq, strideQ, 0, K, ldk, strideK, 0, V, ldv, strideV, 0, O, ldo, strideO, 0, batch,
+                            1, Sq, Sk, D, scale, dtype, stream);
+}
+
+int sf_layer_norm(const void* x, void* y, int64_t rows, int64_t cols, const void* gamma, const void* beta,
+                  float eps, const void* mod_scale, const void* mod_shift, int64_t mod_ld, int64_t group_rows,
+                  float* mean_out, float* rstd_out, sf_dtype dt, void* stream) {
+  g_err[0] = 0;
+  if (!valid_dtype(dt)) return fail(SF_ERR_INVALID_ARG, "sf_layer_norm: unknown dtype %d", (int)dt);
+  if (rows < 0 || cols < 0) return fail(SF_ERR_INVALID_ARG, "sf_layer_norm: negative size");
+  if (rows == 0) return SF_OK;
+  if (cols == 0) return fail(SF_ERR_INVALID_ARG, "sf_layer_norm: normalising over zero columns");
+  if (cols > INT32_MAX) return fail(SF_ERR_UNSUPPORTED, "sf_layer_norm: cols must be < 2^31");
+  if (x == nullptr || y == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_layer_norm: null pointer");
+  if (!(eps >= 0.0f)) return fail(SF_ERR_INVALID_ARG, "sf_layer_norm: eps must be >= 0");
+  const bool mod = mod_scale != nullptr || mod_shift != nullptr;
+  if (mod && (mod_ld < cols || group_rows < 1))
+    return fail(SF_ERR_INVALID_ARG, "sf_layer_norm: modulation needs mod_ld >= cols and group_rows >= 1 "
+                "(mod_ld=%lld group_rows=%lld)", (long long)mod_ld, (long long)group_rows);
+  NormArgs a;
+  a.x = x; a.y = y; a.gamma = gamma; a.beta = beta;
+  a.mscale = mod_scale; a.mshift = mod_shift;
+  a.mean_out = mean_out; a.rstd_out = rstd_out;
+  a.rows = rows; a.cols = cols; a.mld = mod ? mod_ld : 0; a.group_rows = mod ? group_rows : 1;
+  a.eps = eps; a.rms = false;
+  return launch_norm(a, dt, static_cast<hipStream_t>(stream));
+}
+
+int sf_rms_norm(const void* x, void* y, int64_t rows, int64_t cols, const void* gamma, float eps, sf_dtype dt,
+                void* stream) {
+  g_err[0] = 0;
+  if (!valid_dtype(dt)) return fail(SF_ERR_INVALID_ARG, "sf_rms_norm: unknown dtype %d", (int)dt);
+  if (rows < 0 || cols < 0) return fail(SF_ERR_INVALID_ARG, "sf_rms_norm: negative size");
+  if (rows == 0) return SF_OK;
+  if (cols == 0) return fail(SF_ERR_INVALID_ARG, "sf_rms_norm: normalising over zero columns");
+  if (cols > INT32_MAX) return fail(SF_ERR_UNSUPPORTED, "sf_rms_norm: cols must be < 2^31");
+  if (x == nullptr || y == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_rms_norm: null pointer");
+  if (!(eps >= 0.0f)) return fail(SF_ERR_INVALID_ARG, "sf_rms_norm: eps must be >= 0");
+  NormArgs a;
+  a.x = x; a.y = y; a.gamma = gamma; a.beta = nullptr;
+  a.mscale = nullptr; a.mshift = nullptr;
+  a.mean_out = nullptr; a.rstd_out = nullptr;
+  a.rows = rows; a.cols = cols; a.mld = 0; a.group_rows = 1;
+  a.eps = eps; a.rms = true;
+  return launch_norm(a, dt, static_cast<hipStream_t>(stream));
+}
+
+int sf_add(const void* a, const void* b, void* y, int64_t n, sf_dtype dt, void* stream) {
+  g_err[0] = 0;
+  if (!valid_dtype(dt)) return fail(SF_ERR_INVALID_ARG, "sf_add: unknown dtype %d", (int)dt);
+  if (n < 0) return fail(SF_ERR_INVALID_ARG, "sf_add: negative size");
+  if (n == 0) return SF_OK;
+  if (a == nullptr || b == nullptr || y == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_add: null pointer");
+  return launch_add(a, b, y, n, dt, static_cast<hipStream_t>(stream));
 }
 
 int sf_sum_dim(const void* x, void* out, int64_t outer, int64_t dim_size, int64_t inner, sf_dtype in_dtype,

@@ -4,27 +4,24 @@
 
 namespace sf {
 
-int launch_attention(const void* Q, const void* K, const void* V, void* O, int64_t batch, int64_t Sq,
-                     int64_t Sk, int64_t sQ, int64_t sK, int64_t sV, int64_t sO, int64_t ldq, int64_t ldk,
-                     int64_t ldv, int64_t ldo, float scale, sf_dtype dt, hipStream_t st) {
+int launch_attention(const AttnShape& a, float scale, sf_dtype dt, hipStream_t st) {
   AttnParams p;
-  p.Q = Q; p.K = K; p.V = V; p.O = O;
-  p.sQ = sQ; p.sK = sK; p.sV = sV; p.sO = sO;
-  p.ldq = (int)ldq; p.ldk = (int)ldk; p.ldv = (int)ldv; p.ldo = (int)ldo;
-  p.Sq = (int)Sq; p.Sk = (int)Sk;
+  p.Q = a.Q; p.K = a.K; p.V = a.V; p.O = a.O;
+  p.sQ = a.sQ; p.sK = a.sK; p.sV = a.sV; p.sO = a.sO;
+  p.hQ = a.hQ; p.hK = a.hK; p.hV = a.hV; p.hO = a.hO;
+  p.H = (int)a.heads;
+  p.ldq = (int)a.ldq; p.ldk = (int)a.ldk; p.ldv = (int)a.ldv; p.ldo = (int)a.ldo;
+  p.Sq = (int)a.Sq; p.Sk = (int)a.Sk;
   p.scale_log2e = scale * 1.4426950408889634f;
-  const unsigned gx = (unsigned)((Sq + 255) / 256);
-  for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
-    const int64_t nb = (batch - b0) < 65535 ? (batch - b0) : 65535;
-    AttnParams q = p;
-    q.Q = static_cast<const uint16_t*>(Q) + b0 * sQ;
-    q.K = static_cast<const uint16_t*>(K) + b0 * sK;
-    q.V = static_cast<const uint16_t*>(V) + b0 * sV;
-    q.O = static_cast<uint16_t*>(O) + b0 * sO;
+  const unsigned gx = (unsigned)((a.Sq + 255) / 256);
+  const int64_t pairs = a.batch * a.heads;
+  for (int64_t y0 = 0; y0 < pairs; y0 += 65535) {
+    const int64_t ny = (pairs - y0) < 65535 ? (pairs - y0) : 65535;
+    p.y0 = y0;
     if (dt == SF_F16)
-      hipLaunchKernelGGL((attn64_kernel<F16>), dim3(gx, (unsigned)nb), dim3(256), 0, st, q);
+      hipLaunchKernelGGL((attn64_kernel<F16>), dim3(gx, (unsigned)ny), dim3(256), 0, st, p);
     else
-      hipLaunchKernelGGL((attn64_kernel<BF16>), dim3(gx, (unsigned)nb), dim3(256), 0, st, q);
+      hipLaunchKernelGGL((attn64_kernel<BF16>), dim3(gx, (unsigned)ny), dim3(256), 0, st, p);
     const int rc = check_launch("attention");
     if (rc != SF_OK) return rc;
   }

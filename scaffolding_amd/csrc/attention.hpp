@@ -25,7 +25,11 @@
 // keys 4g..4g+3 and 16+4g..16+4g+3 of each 32-key chunk), and the V
 // fragment reads use the same key order, so P never moves between lanes.
 // The 2 GB score and probability tensors of the three-kernel path are never
-// written.  Requires head size 64, Sk % 64 == 0, 16-byte aligned rows.
+// written.  Requires head size 64, scale > 0 and 16-byte aligned rows; a
+// partial last key block is masked.  grid.y runs over (batch, head) pairs,
+// each with its own batch and head offsets, so Q/K/V can be read in place
+// from a packed [batch, S, 3 * heads * 64] projection and O written straight
+// into [batch, Sq, heads * 64] (no head split or merge copies).
 #pragma once
 
 #include "gemm16nt_pp.hpp"
@@ -38,9 +42,12 @@ struct AttnParams {
   const void* V;
   void* O;
   int64_t sQ, sK, sV, sO;      // batch strides, elements
+  int64_t hQ, hK, hV, hO;      // head strides, elements
+  int64_t y0;                  // first (batch, head) pair of this launch
+  int H;                       // heads per batch entry
   int ldq, ldk, ldv, ldo;      // row strides, elements
   int Sq, Sk;
-  float scale_log2e;           // scale * log2(e)
+  float scale_log2e;           // scale * log2(e), > 0
 };
 
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }
@@ -56,13 +63,17 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t b = blockIdx.y;
+  const int64_t y = p.y0 + blockIdx.y;
+  const int64_t b = y / p.H, h = y - b * p.H;
   const int q0 = blockIdx.x * 256 + wave * 64;
   const int Sq = p.Sq, Sk = p.Sk;
-  const int NB = Sk / KB;
-  const uint16_t* Qb = static_cast<const uint16_t*>(p.Q) + b * p.sQ;
-  const uint16_t* Kb = static_cast<const uint16_t*>(p.K) + b * p.sK;
-  const uint16_t* Vb = static_cast<const uint16_t*>(p.V) + b * p.sV;
+  // Key blocks of 64; a partial last block reads zeros past row Sk (the
+  // buffer bound) and its scores there are masked to -inf.
+  const int NB = (Sk + KB - 1) / KB;
+  const int k_tail = Sk - (NB - 1) * KB;  // valid keys of the last block, 1..64
+  const uint16_t* Qb = static_cast<const uint16_t*>(p.Q) + b * p.sQ + h * p.hQ;
+  const uint16_t* Kb = static_cast<const uint16_t*>(p.K) + b * p.sK + h * p.hK;
+  const uint16_t* Vb = static_cast<const uint16_t*>(p.V) + b * p.sV + h * p.hV;
 
   const __amdgpu_buffer_rsrc_t rK =
       __builtin_amdgcn_make_buffer_rsrc((void*)Kb, (short)0, (int)((uint32_t)Sk * (uint32_t)p.ldk * 2u), 0x00020000);
@@ -154,6 +165,19 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
         kf1 = nk1;
       }
     });
+
+    // ---- keys past Sk (last block only) ----------------------------------
+    // Lane l holds keys 16 nb + 4 (l >> 4) + q of the block; scale > 0, so
+    // -inf stays -inf through the scaling and exp2 gives 0.
+    if (k_tail < KB && j == NB - 1) {
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (nb * 16 + 4 * (lane >> 4) + q >= k_tail)
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) s[mb][nb][q] = -INFINITY;
+    }
 
     // ---- online softmax with lazy rescale --------------------------------
     // Each lane checks its 16 scores of each row against the row's current
@@ -250,7 +274,7 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
     });
   }
 
-  uint16_t* Ob = static_cast<uint16_t*>(p.O) + b * p.sO;
+  uint16_t* Ob = static_cast<uint16_t*>(p.O) + b * p.sO + h * p.hO;
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
     const float inv = 1.0f / osum[mb][0];

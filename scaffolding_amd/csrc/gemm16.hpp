@@ -61,6 +61,11 @@ struct GemmParams {
   int full_tiles, split;
   float* ws;
   int* counters;
+  // Residual added after the activation, R[b] M x N of the output dtype
+  // (row stride ldr, batch stride sR; NULL: none).  R may be C itself
+  // (same pointer and ldc): every element is read before it is written.
+  const void* res;
+  int64_t ldr, sR;
 };
 
 // 16-byte global store with the sc0 sc1 cache-policy bits: the agent-scope
@@ -159,6 +164,43 @@ __device__ __forceinline__ void load_bias4(const void* bias, int n, int N, float
   const uint16_t* bp = static_cast<const uint16_t*>(bias);
 #pragma unroll
   for (int q = 0; q < 4; ++q) b[q] = (n + q < N) ? Elem<TIn>::to_f32(bp[n + q]) : 0.0f;
+}
+
+// Residual values R[m][n..n+3] (dtype = output dtype TOut) as fp32, zeros
+// past N; `vec`: 8-byte (16-bit) / 16-byte (fp32) aligned rows.
+template <typename TOut> struct Res4 {  // 16-bit outputs
+  __device__ __forceinline__ static void load(const void* R, int64_t row_off, int n, int N, bool vec,
+                                              float r[4]) {
+    const uint16_t* rrow = static_cast<const uint16_t*>(R) + row_off;
+    if (vec && n + 3 < N) {
+      const u32x2 w = *reinterpret_cast<const u32x2*>(rrow + n);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) r[q] = Elem<TOut>::to_f32(static_cast<uint16_t>(w[q >> 1] >> ((q & 1) * 16)));
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) r[q] = (n + q < N) ? Elem<TOut>::to_f32(rrow[n + q]) : 0.0f;
+    }
+  }
+};
+template <> struct Res4<float> {
+  __device__ __forceinline__ static void load(const void* R, int64_t row_off, int n, int N, bool vec,
+                                              float r[4]) {
+    const float* rrow = static_cast<const float*>(R) + row_off;
+    if (vec && n + 3 < N) {
+      const f32x4 w = *reinterpret_cast<const f32x4*>(rrow + n);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) r[q] = w[q];
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) r[q] = (n + q < N) ? rrow[n + q] : 0.0f;
+    }
+  }
+};
+// Whether Res4 may use vector loads on R (rows aligned for 4 elements).
+template <typename TOut>
+__device__ __forceinline__ bool res_vec_ok(const void* R, int64_t ldr) {
+  constexpr int E = sizeof(typename Elem<TOut>::storage);
+  return ((ldr & 3) == 0) && ((reinterpret_cast<uintptr_t>(R) & (4 * E - 1)) == 0);
 }
 
 template <typename TIn, typename TOut, int BM, int BN, int WAVES_M, int WAVES_N, bool B_KMAJOR,
@@ -392,6 +434,8 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmParam
   const int act = epi_act(p.epi);
   const float alpha = p.alpha;
   const bool vec_ok = ((p.ldc & 3) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
+  const void* R = p.res != nullptr ? static_cast<const OutS*>(p.res) + b * p.sR : nullptr;
+  const bool rvec = R != nullptr && res_vec_ok<TOut>(R, p.ldr);
   with_act(act, [&](auto act_c) {
     constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
@@ -406,6 +450,12 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmParam
           float v[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) v[q] = act_t<ACT>(acc[i][j][q] * alpha + bv[q]);
+          if (R != nullptr) {
+            float r[4];
+            Res4<TOut>::load(R, (int64_t)m * p.ldr, n, N, rvec, r);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] += r[q];
+          }
           Store4<TOut>::run(C + (int64_t)m * p.ldc, n, N, vec_ok, v);
         }
       }

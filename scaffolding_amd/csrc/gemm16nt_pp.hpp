@@ -415,6 +415,11 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   constexpr int ROWS_I = 64 / LANES_ROW;
   uint16_t* C = static_cast<uint16_t*>(p.C) + b * p.sC;
   const bool vec_ok = ((p.ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
+  // Residual: read in the accumulator layout (4 consecutive columns of one
+  // row per lane) and added before the single rounding.  R may be C: every
+  // element of R is read in a pass before that pass stores it.
+  const void* R = p.res != nullptr ? static_cast<const uint16_t*>(p.res) + b * p.sR : nullptr;
+  const bool rvec = R != nullptr && res_vec_ok<TOut>(R, p.ldr);
   with_act(act, [&](auto act_c) {
   constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
@@ -429,6 +434,15 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
         float v[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[q] = act_t<ACT>(acc[i][j][q] * alpha + bv[i][q]);
+        if (R != nullptr) {
+          const int gm = m0 + wm * WM + j * 16 + (lane & 15);
+          if (gm < M) {
+            float rr[4];
+            Res4<TOut>::load(R, (int64_t)gm * p.ldr, n0 + wn * WN + i * 16 + 4 * (lane >> 4), N, rvec, rr);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] += rr[q];
+          }
+        }
         const uint32_t lo = pack2<TOut>(v[0], v[1]);
         const uint32_t hi = pack2<TOut>(v[2], v[3]);
         *reinterpret_cast<u32x2*>(stage + r * PITCH + (i * 16 + 4 * (lane >> 4)) * 2) = u32x2{lo, hi};

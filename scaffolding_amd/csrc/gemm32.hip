@@ -33,6 +33,7 @@ int launch_gemm32(bool a_kmajor, bool b_kmajor, int cfg, const GemmParams& p, in
     q.A = static_cast<const float*>(p.A) + b0 * p.sA;
     q.B = static_cast<const float*>(p.B) + b0 * p.sB;
     q.C = static_cast<float*>(p.C) + b0 * p.sC;
+    if (p.res != nullptr) q.res = static_cast<const float*>(p.res) + b0 * p.sR;
     const unsigned gy = static_cast<unsigned>(nb);
     const int rc = a_kmajor ? (b_kmajor ? launch32_t<true, true>(cfg, q, gx, gy, st)
                                         : launch32_t<false, true>(cfg, q, gx, gy, st))

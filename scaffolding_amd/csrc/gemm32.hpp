@@ -247,6 +247,8 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm32_kernel(GemmParam
   const float alpha = p.alpha;
   const bool vec_ok = ((p.ldc & 3) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
   const float* bias = static_cast<const float*>(p.bias);
+  const void* R = p.res != nullptr ? static_cast<const float*>(p.res) + b * p.sR : nullptr;
+  const bool rvec = R != nullptr && res_vec_ok<float>(R, p.ldr);
   with_act(act, [&](auto act_c) {
     constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
@@ -264,6 +266,12 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm32_kernel(GemmParam
           float v[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) v[q] = act_t<ACT>(acc[i][j][q] * alpha + bv[q]);
+          if (R != nullptr) {
+            float r[4];
+            Res4<float>::load(R, (int64_t)m * p.ldr, n, N, rvec, r);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] += r[q];
+          }
           Store4<float>::run(C + (int64_t)m * p.ldc, n, N, vec_ok, v);
         }
       }

@@ -42,9 +42,37 @@ int launch_gemm32(bool a_kmajor, bool b_kmajor, int cfg, const GemmParams& p, in
 // Tile edge of a config (BM, BN).
 void tile_dims(int cfg, bool fp32, int& bm, int& bn);
 
-int launch_attention(const void* Q, const void* K, const void* V, void* O, int64_t batch, int64_t Sq,
-                     int64_t Sk, int64_t sQ, int64_t sK, int64_t sV, int64_t sO, int64_t ldq, int64_t ldk,
-                     int64_t ldv, int64_t ldo, float scale, sf_dtype dt, hipStream_t st);
+// Operands of one fused attention call (element strides): pair (b, h)
+// reads Q + b sQ + h hQ (rows of ldq), likewise K, V, and writes O.
+struct AttnShape {
+  const void* Q;
+  const void* K;
+  const void* V;
+  void* O;
+  int64_t ldq, ldk, ldv, ldo;
+  int64_t sQ, sK, sV, sO;
+  int64_t hQ, hK, hV, hO;
+  int64_t batch, heads, Sq, Sk;
+};
+int launch_attention(const AttnShape& a, float scale, sf_dtype dt, hipStream_t st);
+// Layer norm (rms = false: centred, gamma and beta, optional per-group
+// modulation y = h (1 + scale) + shift) or RMS norm (rms = true: gamma
+// only) over `rows` contiguous rows of `cols` elements.
+struct NormArgs {
+  const void* x;
+  void* y;
+  const void* gamma;
+  const void* beta;
+  const void* mscale;
+  const void* mshift;
+  float* mean_out;
+  float* rstd_out;
+  int64_t rows, cols, mld, group_rows;
+  float eps;
+  bool rms;
+};
+int launch_norm(const NormArgs& a, sf_dtype dt, hipStream_t st);
+int launch_add(const void* a, const void* b, void* y, int64_t n, sf_dtype dt, hipStream_t st);
 int launch_softmax(const void* x, void* y, int64_t rows, int64_t cols, sf_dtype in, sf_dtype out,
                    float scale, hipStream_t st);
 int launch_unary(int op, const void* x, void* y, int64_t n, sf_dtype dt, float s, hipStream_t st);

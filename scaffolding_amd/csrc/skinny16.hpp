@@ -98,6 +98,8 @@ __global__ __launch_bounds__(KSPLIT * 64) void skinny16_kernel(GemmParams p) {
   const bool has_bias = epi_has_bias(p.epi);
   const int act = epi_act(p.epi);
   const bool vec_ok = ((p.ldc & 3) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
+  const void* R = p.res != nullptr ? static_cast<const OutS*>(p.res) + b * p.sR : nullptr;
+  const bool rvec = R != nullptr && res_vec_ok<TOut>(R, p.ldr);
   const int m = lane & 15;
   if (m >= M) return;
   with_act(act, [&](auto act_c) {
@@ -111,6 +113,12 @@ __global__ __launch_bounds__(KSPLIT * 64) void skinny16_kernel(GemmParams p) {
       float v[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) v[q] = act_t<ACT>(acc[j][q] * p.alpha + bv[q]);
+      if (R != nullptr) {
+        float r[4];
+        Res4<TOut>::load(R, (int64_t)m * p.ldr, n, N, rvec, r);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] += r[q];
+      }
       Store4<TOut>::run(C + (int64_t)m * p.ldc, n, N, vec_ok, v);
     }
   });
@@ -293,11 +301,16 @@ __global__ __launch_bounds__(NW * 64) void skinny16l_kernel(GemmParams p) {
   const bool vec_ok = ((p.ldc & 3) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
   float bv[4] = {0.f, 0.f, 0.f, 0.f};
   if (has_bias) load_bias4<TIn>(p.bias, n, n_end, bv);
+  float rv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (p.res != nullptr) {
+    const void* Rb = static_cast<const OutS*>(p.res) + b * p.sR;
+    Res4<TOut>::load(Rb, (int64_t)m * p.ldr, n, n_end, res_vec_ok<TOut>(Rb, p.ldr), rv);
+  }
   with_act(epi_act(p.epi), [&](auto act_c) {
     constexpr int ACT = decltype(act_c)::value;
     float v[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) v[q] = act_t<ACT>(sum[q] * p.alpha + bv[q]);
+    for (int q = 0; q < 4; ++q) v[q] = act_t<ACT>(sum[q] * p.alpha + bv[q]) + rv[q];
     Store4<TOut>::run(C + (int64_t)m * p.ldc, n, n_end, vec_ok, v);
   });
 }

@@ -1,6 +1,8 @@
-"""nn surface of the path: Module, Parameter, Linear, SiLU, GELU and the
-functional ops (reference nn/__init__.py)."""
+"""nn surface of the path: Module, Parameter, Sequential, Linear, LayerNorm,
+RMSNorm, Dropout, SiLU, GELU and the functional ops (reference
+nn/__init__.py)."""
 from . import functional
-from .layers import GELU, Linear, Module, Parameter, SiLU
+from .layers import GELU, Dropout, LayerNorm, Linear, Module, Parameter, RMSNorm, Sequential, SiLU
 
-__all__ = ["functional", "Module", "Parameter", "Linear", "SiLU", "GELU"]
+__all__ = ["functional", "Module", "Parameter", "Sequential", "Linear", "LayerNorm", "RMSNorm", "Dropout",
+           "SiLU", "GELU"]

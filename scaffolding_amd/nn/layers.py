@@ -1,5 +1,6 @@
-"""Module, Parameter, Linear, SiLU, GELU (reference nn/module.py,
-nn/parameter.py, nn/layers.py:59-151, :358-440).
+"""Module, Parameter, Sequential, Linear, LayerNorm, RMSNorm, Dropout, SiLU,
+GELU (reference nn/module.py, nn/parameter.py, nn/layers.py:59-151,
+:339-440, :443-585).
 
 Only the GPU-resident forward of the reference's Linear exists here
 (reference nn/layers.py:85-110): weights are uploaded once, on construction
@@ -88,23 +89,49 @@ class Module:
         return self
 
     def state_dict(self) -> dict:
-        return {n: p.numpy() for n, p in self.named_parameters()}
+        """Parameter name -> the Parameter itself, in registration order
+        (reference nn/module.py:136-154: the dict holds the parameters, not
+        copies; .numpy() of a value downloads it)."""
+        return dict(self.named_parameters())
 
-    def load_state_dict(self, state: dict) -> None:
+    def load_state_dict(self, state_dict: dict, strict: bool = True) -> None:
+        """reference nn/module.py:156-185: each key naming one of this
+        module's parameters replaces that parameter's data in place (the
+        Parameter object is kept); keys naming nothing are ignored and
+        parameters the dict does not name keep their data (the reference
+        takes `strict` and never raises).  Values are NumPy arrays or
+        Tensors.  A parameter on the GPU receives them without a host copy
+        being kept: host arrays are uploaded as float32 and rounded to the
+        parameter's dtype on the device (bfloat16 / float16 by RNE, sf_cast);
+        device tensors are copied (and cast) device-side.  Unlike the
+        reference, a value whose shape differs from the parameter's raises
+        ValueError instead of being uploaded as is."""
         own = dict(self.named_parameters())
-        missing = set(own) - set(state)
-        if missing:
-            raise KeyError("missing keys: %s" % sorted(missing))
-        for name, arr in state.items():
-            target = own[name]
-            owner = self
-            parts = name.split(".")
-            for part in parts[:-1]:
-                owner = owner._modules[part]
-            if tuple(np.shape(arr)) != target.shape:
-                raise ValueError("shape mismatch for %s: %s vs %s" % (name, np.shape(arr), target.shape))
-            setattr(owner, parts[-1], Parameter(Tensor(arr, dtype=target.dtype, device=target.device),
-                                                requires_grad=target.requires_grad))
+        for name, val in state_dict.items():
+            target = own.get(name)
+            if target is None:
+                continue
+            shape = tuple(val.shape) if isinstance(val, Tensor) else tuple(np.shape(val))
+            if shape != target.shape:
+                raise ValueError("load_state_dict: shape mismatch for %s: %s vs %s" % (name, shape, target.shape))
+            if target._gpu is None:
+                host = val.numpy() if isinstance(val, Tensor) else np.asarray(val)
+                target._data = np.array(host, dtype=target._dtype.to_numpy(), copy=True)
+                continue
+            dev = target._gpu.device_id
+            storage = target._dtype.device_storage()
+            if isinstance(val, Tensor) and val._gpu is not None:
+                src = val._gpu if val._gpu.device_id == dev else _cuops.gputensor_to_device(val._gpu, dev)
+                if _cuops.resolve_dtype(src.dtype) == _cuops.resolve_dtype(storage):
+                    dst = _cuops.empty(tuple(src.shape), storage, dev)
+                    _cuops.dev_copy(src, dst)
+                else:
+                    dst = _cuops.dev_cast(src, storage)
+            else:
+                host = val.numpy() if isinstance(val, Tensor) else np.asarray(val)
+                dst = _cuops.gputensor_from_numpy(np.ascontiguousarray(host, dtype=np.float32), dev, storage)
+            target._gpu = dst
+            target._data = None
 
 
 class Linear(Module):
@@ -131,27 +158,127 @@ class Linear(Module):
         else:
             self.bias = None
 
-    def forward(self, x: Tensor, activation: str | None = None) -> Tensor:
+    def forward(self, x: Tensor, activation: str | None = None, residual: Tensor | None = None) -> Tensor:
+        """``residual`` (shape of the output) is added in the same launch,
+        after the activation: y = act(x W^T + b) + residual."""
         act = activation if activation is not None else self.activation
-        return _linear(x, self.weight, self.bias, act)
+        return _linear(x, self.weight, self.bias, act, residual)
 
     def __repr__(self) -> str:
         return "Linear(in_features=%d, out_features=%d, bias=%s)" % (
             self.in_features, self.out_features, self.bias is not None)
 
 
-def _linear(x: Tensor, weight: Tensor, bias: Tensor | None, act: str | None) -> Tensor:
-    if x._gpu is None or weight._gpu is None or (bias is not None and bias._gpu is None):
+def _on(t: Tensor | None, dev: int):
+    """t's GpuTensor on device `dev` (copied there if it lives elsewhere)."""
+    if t is None:
+        return None
+    return t._gpu if t._gpu.device_id == dev else _cuops.gputensor_to_device(t._gpu, dev)
+
+
+def _linear(x: Tensor, weight: Tensor, bias: Tensor | None, act: str | None,
+            residual: Tensor | None = None) -> Tensor:
+    if x._gpu is None or weight._gpu is None or (bias is not None and bias._gpu is None) or \
+            (residual is not None and residual._gpu is None):
         _gpu_only("linear")
     dev = x._gpu.device_id
-    w_gt = weight._gpu
-    if w_gt.device_id != dev:
-        w_gt = _cuops.gputensor_to_device(w_gt, dev)
-    b_gt = None
-    if bias is not None:
-        b_gt = bias._gpu if bias._gpu.device_id == dev else _cuops.gputensor_to_device(bias._gpu, dev)
     _cuops.set_device(dev)
-    return Tensor._wrap_gpu(_cuops.dev_linear_forward(x._gpu, w_gt, b_gt, act), x._device)
+    out = _cuops.dev_linear_forward(x._gpu, _on(weight, dev), _on(bias, dev), act, _on(residual, dev))
+    return Tensor._wrap_gpu(out, x._device)
+
+
+class Sequential(Module):
+    """Children run in order, registered as "0", "1", ... so state_dict keys
+    match the reference's (reference nn/module.py:345-367)."""
+
+    def __init__(self, *modules):
+        super().__init__()
+        object.__setattr__(self, "_seq", list(modules))
+        for i, m in enumerate(modules):
+            self._modules[str(i)] = m
+
+    def forward(self, x):
+        for m in self._seq:
+            x = m(x)
+        return x
+
+    def __len__(self) -> int:
+        return len(self._seq)
+
+    def __getitem__(self, idx):
+        return self._seq[idx]
+
+    def __iter__(self):
+        return iter(self._seq)
+
+
+class Dropout(Module):
+    """Identity in eval mode or at p = 0 (reference nn/layers.py:339-353);
+    random dropout is not on the device path."""
+
+    def __init__(self, p: float = 0.5):
+        super().__init__()
+        self.p = p
+
+    def forward(self, x: Tensor) -> Tensor:
+        if not self.training or self.p == 0.0:
+            return x
+        raise NotImplementedError("Dropout with p > 0 in training mode is not on the device path")
+
+
+class LayerNorm(Module):
+    """Layer normalisation over the last dim (reference nn/layers.py:443-521):
+    weight ones and bias zeros of shape (dim,), eps 1e-5; one launch of
+    sf_layer_norm, result in the input dtype."""
+
+    def __init__(self, normalized_shape, eps: float = 1e-5, elementwise_affine: bool = True, device=None,
+                 dtype=None):
+        super().__init__()
+        if isinstance(normalized_shape, int):
+            normalized_shape = (normalized_shape,)
+        if len(normalized_shape) != 1:
+            raise NotImplementedError("LayerNorm over more than the last dim is not on the device path")
+        self.normalized_shape = tuple(normalized_shape)
+        self.eps = eps
+        self.elementwise_affine = elementwise_affine
+        dev = device or "cuda"
+        if elementwise_affine:
+            self.weight = Parameter(np.ones(self.normalized_shape, np.float32), dtype=dtype, device=dev)
+            self.bias = Parameter(np.zeros(self.normalized_shape, np.float32), dtype=dtype, device=dev)
+        else:
+            self.weight = None
+            self.bias = None
+
+    def forward(self, x: Tensor) -> Tensor:
+        if x._gpu is None:
+            _gpu_only("layer_norm")
+        dev = x._gpu.device_id
+        _cuops.set_device(dev)
+        w = _on(self.weight, dev) if self.weight is not None else None
+        b = _on(self.bias, dev) if self.bias is not None else None
+        return Tensor._wrap_gpu(_cuops.dev_layer_norm(x._gpu, w, b, self.eps), x._device)
+
+
+class RMSNorm(Module):
+    """RMS normalisation over the last dim (reference nn/layers.py:529-585):
+    weight ones of shape (dim,), eps 1e-6."""
+
+    def __init__(self, normalized_shape, eps: float = 1e-6, device=None, dtype=None):
+        super().__init__()
+        if isinstance(normalized_shape, int):
+            normalized_shape = (normalized_shape,)
+        if len(normalized_shape) != 1:
+            raise NotImplementedError("RMSNorm over more than the last dim is not on the device path")
+        self.normalized_shape = tuple(normalized_shape)
+        self.eps = eps
+        self.weight = Parameter(np.ones(self.normalized_shape, np.float32), dtype=dtype, device=device or "cuda")
+
+    def forward(self, x: Tensor) -> Tensor:
+        if x._gpu is None:
+            _gpu_only("rms_norm")
+        dev = x._gpu.device_id
+        _cuops.set_device(dev)
+        return Tensor._wrap_gpu(_cuops.dev_rms_norm(x._gpu, _on(self.weight, dev), self.eps), x._device)
 
 
 class SiLU(Module):
@@ -175,4 +302,5 @@ class GELU(Module):
         return gelu(x)
 
 
-__all__ = ["Module", "Parameter", "Linear", "SiLU", "GELU", "_device_t", "_dtype_t"]
+__all__ = ["Module", "Parameter", "Sequential", "Linear", "LayerNorm", "RMSNorm", "Dropout", "SiLU", "GELU",
+           "_device_t", "_dtype_t"]

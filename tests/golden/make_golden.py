@@ -13,6 +13,14 @@ here independently of NumPy's BLAS:
   tiny_backward.npz    tiny linear-layer gradients (grad_input = g W,
                        grad_weight = g^T x, grad_bias = column sums of g)
                        by triple loops / column loops in math.fsum
+  tiny_norm.npz        tiny layer norms (with gamma, beta and a per-row
+                       adaptive scale / shift) and RMS norms, row by row in
+                       math.fsum, and tiny single-head attentions (ragged
+                       key counts) with fsum dot products and softmax sums
+  tiny_dit.npz         one tiny DiT block (self-attention, cross-attention
+                       and the SiLU MLP, reference diffusion/models.py:538-590)
+                       evaluated in pure Python lists with math.fsum: every
+                       linear, norm, head split, softmax and residual
   config_inputs.json   shape, dtype and SHA-256 of every generated input of
                        BASELINE.json's five configs (oracle.configs), so the
                        generators are pinned across machines
@@ -110,6 +118,146 @@ def tiny_backward():
     np.savez(os.path.join(HERE, "tiny_backward.npz"), **arrays)
 
 
+def lnorm_rows(x, gamma, beta, eps, ms=None, mt=None):
+    out = []
+    for r, row in enumerate(x):
+        n = len(row)
+        mu = math.fsum(row) / n
+        var = math.fsum((v - mu) ** 2 for v in row) / n
+        rs = 1.0 / math.sqrt(var + eps)
+        y = []
+        for j, v in enumerate(row):
+            h = (v - mu) * rs * gamma[j] + beta[j]
+            if ms is not None:
+                h = h * (1.0 + ms[r][j]) + mt[r][j]
+            y.append(h)
+        out.append(y)
+    return out
+
+
+def attn_rows(q, k, v, scale):
+    out = []
+    for qi in q:
+        s = [scale * math.fsum(a * b for a, b in zip(qi, kj)) for kj in k]
+        m = max(s)
+        e = [math.exp(t - m) for t in s]
+        z = math.fsum(e)
+        out.append([math.fsum(e[j] * v[j][d] for j in range(len(k))) / z for d in range(len(v[0]))])
+    return out
+
+
+def tiny_norm():
+    rng = np.random.default_rng(512)
+    arrays = {}
+    for (r, c) in [(1, 1), (3, 5), (4, 16), (2, 37)]:
+        x = rng.uniform(-3, 3, (r, c)) + rng.uniform(-2, 2, (r, 1))
+        g = rng.uniform(0.5, 1.5, c)
+        b = rng.uniform(-0.5, 0.5, c)
+        ms = rng.uniform(-0.5, 0.5, (r, c))
+        mt = rng.uniform(-0.5, 0.5, (r, c))
+        key = "ln_%dx%d" % (r, c)
+        arrays[key + "_x"], arrays[key + "_g"], arrays[key + "_b"] = x, g, b
+        arrays[key + "_ms"], arrays[key + "_mt"] = ms, mt
+        xl = x.tolist()
+        arrays[key + "_y"] = np.array(lnorm_rows(xl, g.tolist(), b.tolist(), 1e-5))
+        arrays[key + "_ymod"] = np.array(lnorm_rows(xl, g.tolist(), b.tolist(), 1e-5, ms.tolist(), mt.tolist()))
+        rms = []
+        for row in xl:
+            den = math.sqrt(math.fsum(v * v for v in row) / len(row) + 1e-6)
+            rms.append([v / den * g[j] for j, v in enumerate(row)])
+        arrays["rms_%dx%d_y" % (r, c)] = np.array(rms)
+    for (n, s, d) in [(1, 1, 4), (3, 5, 8), (4, 67, 8)]:
+        q = rng.uniform(-1, 1, (n, d))
+        k = rng.uniform(-1, 1, (s, d))
+        v = rng.uniform(-1, 1, (s, d))
+        key = "attn_%dx%dx%d" % (n, s, d)
+        arrays[key + "_q"], arrays[key + "_k"], arrays[key + "_v"] = q, k, v
+        arrays[key + "_o"] = np.array(attn_rows(q.tolist(), k.tolist(), v.tolist(), 1.0 / math.sqrt(d)))
+    np.savez(os.path.join(HERE, "tiny_norm.npz"), **arrays)
+
+
+def tiny_dit():
+    """B = 1, N = 3 tokens, C = 4 (2 heads of 2), cond_dim 3, context of 2
+    tokens of width 5, MLP hidden 16."""
+    rng = np.random.default_rng(538)
+    N, C, H, CD, S, XD = 3, 4, 2, 3, 2, 5
+    D = C // H
+    p = {}
+
+    def lin(name, i, o, bias=True):
+        p[name + ".weight"] = rng.uniform(-0.6, 0.6, (o, i))
+        if bias:
+            p[name + ".bias"] = rng.uniform(-0.2, 0.2, o)
+
+    for nm in ("norm1", "norm2", "norm3"):
+        p[nm + ".norm.weight"] = rng.uniform(0.7, 1.3, C)
+        p[nm + ".norm.bias"] = rng.uniform(-0.2, 0.2, C)
+        lin(nm + ".linear", CD, 2 * C)
+    lin("to_qkv", C, 3 * C, bias=False)
+    lin("self_out", C, C)
+    lin("cross_q", C, C, bias=False)
+    lin("cross_k", XD, C, bias=False)
+    lin("cross_v", XD, C, bias=False)
+    lin("cross_out", C, C)
+    lin("ff.0", C, 4 * C)
+    lin("ff.3", 4 * C, C)
+    x = rng.uniform(-2, 2, (1, N, C))
+    cond = rng.uniform(-1, 1, (1, CD))
+    ctx = rng.uniform(-1, 1, (1, S, XD))
+
+    L = {k: v.tolist() for k, v in p.items()}
+
+    def linear(rows, name, act=None):
+        w = L[name + ".weight"]
+        b = L.get(name + ".bias")
+        out = []
+        for r in rows:
+            y = []
+            for j, wj in enumerate(w):
+                t = math.fsum(a * c for a, c in zip(r, wj)) + (b[j] if b is not None else 0.0)
+                y.append(t / (1.0 + math.exp(-t)) if act == "silu" else t)
+            out.append(y)
+        return out
+
+    def ada(rows, nm):
+        prm = linear(cond.tolist(), nm + ".linear")[0]
+        ms = [prm[:C]] * len(rows)
+        mt = [prm[C:]] * len(rows)
+        return lnorm_rows(rows, L[nm + ".norm.weight"], L[nm + ".norm.bias"], 1e-5, ms, mt)
+
+    def mha(qr, kr, vr):
+        out = [[0.0] * C for _ in qr]
+        for h in range(H):
+            sl = slice(h * D, (h + 1) * D)
+            o = attn_rows([r[sl] for r in qr], [r[sl] for r in kr], [r[sl] for r in vr], 1.0 / math.sqrt(D))
+            for i, row in enumerate(o):
+                out[i][sl] = row
+        return out
+
+    xr = x[0].tolist()
+    h = ada(xr, "norm1")
+    qkv = linear(h, "to_qkv")
+    sa = mha([r[:C] for r in qkv], [r[C:2 * C] for r in qkv], [r[2 * C:] for r in qkv])
+    so = linear(sa, "self_out")
+    xr = [[a + b for a, b in zip(r1, r2)] for r1, r2 in zip(xr, so)]
+    x_sa = [list(r) for r in xr]
+    h2 = ada(xr, "norm2")
+    ca = mha(linear(h2, "cross_q"), linear(ctx[0].tolist(), "cross_k"), linear(ctx[0].tolist(), "cross_v"))
+    co = linear(ca, "cross_out")
+    xr = [[a + b for a, b in zip(r1, r2)] for r1, r2 in zip(xr, co)]
+    f = linear(ada(xr, "norm3"), "ff.0", "silu")
+    fo = linear(f, "ff.3")
+    y_cross = [[a + b for a, b in zip(r1, r2)] for r1, r2 in zip(xr, fo)]
+    # without the context: FFN straight after self-attention
+    f = linear(ada(x_sa, "norm3"), "ff.0", "silu")
+    fo = linear(f, "ff.3")
+    y_self = [[a + b for a, b in zip(r1, r2)] for r1, r2 in zip(x_sa, fo)]
+    arrays = {"p_" + k: v for k, v in p.items()}
+    arrays.update(x=x, cond=cond, context=ctx, heads=np.array(H), y_self=np.array([y_self]),
+                  y_cross=np.array([y_cross]))
+    np.savez(os.path.join(HERE, "tiny_dit.npz"), **arrays)
+
+
 def digest(a: np.ndarray) -> dict:
     a = np.ascontiguousarray(a, dtype=np.float32)
     return {"shape": list(a.shape), "sha256": hashlib.sha256(a.tobytes()).hexdigest(),
@@ -137,5 +285,7 @@ if __name__ == "__main__":
     tiny_gemm()
     tiny_linear()
     tiny_backward()
+    tiny_norm()
+    tiny_dit()
     config_inputs()
     print("fixtures written to", HERE)

@@ -91,7 +91,9 @@ def test_fused_attention_large_scores_and_leading_dims():
 
 @pytest.mark.parametrize("shape", [(2, 40, 100, 64), (1, 64, 64, 32), (1, 33, 128, 80)],
                          ids=lambda s: "x".join(map(str, s)))
-def test_unsupported_shapes_fall_back(shape):
+def test_other_shapes(shape):
+    """Sk = 100 (fused, masked tail), head sizes 32 and 80 (three-launch
+    path)."""
     b, sq, sk, d = shape
     rng = np.random.default_rng(3)
     q = rnd(rng, (b, sq, d), 1.0, "bfloat16")
@@ -107,15 +109,17 @@ def test_abi_refusals():
     so = ctypes.CDLL(os.path.join(ROOT, "scaffolding_amd", "libsfgemm.so"))
     so.sf_last_error.restype = ctypes.c_char_p
     I64, P = ctypes.c_int64, ctypes.c_void_p
-    x = up(np.zeros((1, 64, 64), np.float32), "float16")
+    # 128 rows: every call below stays inside the buffer (sk <= 128)
+    x = up(np.zeros((1, 128, 64), np.float32), "float16")
     p = P(x.data_ptr)
 
-    def call(d=64, sk=64, dt=1, ld=64):
+    def call(d=64, sk=64, dt=1, ld=64, scale=1.0):
         return so.sf_attention(p, I64(ld), I64(0), p, I64(ld), I64(0), p, I64(ld), I64(0), p, I64(ld), I64(0),
-                               I64(1), I64(64), I64(sk), I64(d), ctypes.c_float(1.0), dt, None)
+                               I64(1), I64(64), I64(sk), I64(d), ctypes.c_float(scale), dt, None)
     assert call() == 0
+    assert call(sk=96) == 0  # a partial last key block is masked
     assert call(d=32) == -3 and b"head size" in so.sf_last_error()
-    assert call(sk=96) == -3 and b"multiple of 64" in so.sf_last_error()
+    assert call(scale=0.0) == -3 and b"scale" in so.sf_last_error()
     assert call(dt=0) == -3 and b"16-bit" in so.sf_last_error()
     assert call(ld=63) == -2
     cu().device_synchronize()
