@@ -166,6 +166,23 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
       }
     });
 
+    // ---- V fragments of the whole block (16 transposing reads) -----------
+    // Issued now, so they land while the row maxima are formed.
+    const uint32_t va = lds_addr(&sV[st][0]) + vfo_base;
+    u32x4 vf[4][2];
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<4>([&](auto dbc) {
+      constexpr int DB = decltype(dbc)::value;
+      const uint32_t a0 = va + (uint32_t)(((2 * DB + vch) ^ vsw) << 4);
+      const u32x2 t00 = ds_read_tr16<0>(a0);
+      const u32x2 t01 = ds_read_tr16<16 * 128>(a0);
+      const u32x2 t10 = ds_read_tr16<32 * 128>(a0);
+      const u32x2 t11 = ds_read_tr16<48 * 128>(a0);
+      vf[DB][0] = u32x4{t00.x, t00.y, t01.x, t01.y};
+      vf[DB][1] = u32x4{t10.x, t10.y, t11.x, t11.y};
+    });
+    __builtin_amdgcn_sched_barrier(0);
+
     // ---- keys past Sk (last block only) ----------------------------------
     // Lane l holds keys 16 nb + 4 (l >> 4) + q of the block; scale > 0, so
     // -inf stays -inf through the scaling and exp2 gives 0.
@@ -213,65 +230,56 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
         for (int db = 0; db < 4; ++db) o[mb][db] *= corr;
       }
     }
+    // ---- P = 2^(S scale - m) packed to 16 bits, O += P V, row sums -------
+    // Row block mb's exponentials (VALU: 16 exp2, 16 FMAs, 8 conversions)
+    // are interleaved with the MFMAs of row block mb - 1 (8 for P V, 2 for
+    // the row sums): the MFMA pipe and the VALU run side by side within
+    // the wave instead of one after the other.
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));  // V fragments landed
+    __builtin_amdgcn_sched_barrier(0);
     u32x4 pf[4][2];
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      const float nm = -mrow[mb];
+    auto expo = [&](auto mb_c) {
+      constexpr int MB = decltype(mb_c)::value;
+      const float nm = -mrow[MB];
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         uint32_t w[4];
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
           for (int q2 = 0; q2 < 2; ++q2) {
-            const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[mb][2 * c + h][2 * q2], sc, nm));
-            const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[mb][2 * c + h][2 * q2 + 1], sc, nm));
-            w[h * 2 + q2] = pack2<T>(e0, e1);
+            const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[MB][2 * c + hh][2 * q2], sc, nm));
+            const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[MB][2 * c + hh][2 * q2 + 1], sc, nm));
+            w[hh * 2 + q2] = pack2<T>(e0, e1);
           }
-        pf[mb][c] = u32x4{w[0], w[1], w[2], w[3]};
+        pf[MB][c] = u32x4{w[0], w[1], w[2], w[3]};
       }
-    }
-
-    // ---- O += P V, V fragments per 16-d block; row sums against ones ------
-    const uint32_t va = lds_addr(&sV[st][0]) + vfo_base;
-    auto vread = [&](int db, u32x4& f0, u32x4& f1) {
-      const uint32_t a0 = va + (uint32_t)(((2 * db + vch) ^ vsw) << 4);
-      const u32x2 t00 = ds_read_tr16<0>(a0);
-      const u32x2 t01 = ds_read_tr16<16 * 128>(a0);
-      const u32x2 t10 = ds_read_tr16<32 * 128>(a0);
-      const u32x2 t11 = ds_read_tr16<48 * 128>(a0);
-      f0 = u32x4{t00.x, t00.y, t01.x, t01.y};
-      f1 = u32x4{t10.x, t10.y, t11.x, t11.y};
     };
-    __builtin_amdgcn_sched_barrier(0);
-    u32x4 vf0, vf1;
-    vread(0, vf0, vf1);
-    __builtin_amdgcn_sched_barrier(0);
+    auto pv = [&](auto mb_c) {
+      constexpr int MB = decltype(mb_c)::value;
+      osum[MB] = Mfma16<T>::run(ones, pf[MB][0], osum[MB]);
+      osum[MB] = Mfma16<T>::run(ones, pf[MB][1], osum[MB]);
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) osum[mb] = Mfma16<T>::run(ones, pf[mb][0], osum[mb]);
+      for (int db = 0; db < 4; ++db) o[MB][db] = Mfma16<T>::run(vf[db][0], pf[MB][0], o[MB][db]);
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) osum[mb] = Mfma16<T>::run(ones, pf[mb][1], osum[mb]);
-    static_for<4>([&](auto dbc) {
-      constexpr int DB = decltype(dbc)::value;
-      u32x4 nv0, nv1;
-      __builtin_amdgcn_sched_barrier(0);
-      if constexpr (DB < 3) {
-        vread(DB + 1, nv0, nv1);
-        __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 4));
-      } else {
-        __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+      for (int db = 0; db < 4; ++db) o[MB][db] = Mfma16<T>::run(vf[db][1], pf[MB][1], o[MB][db]);
+    };
+    expo(std::integral_constant<int, 0>{});
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<3>([&](auto i_c) {
+      constexpr int I = decltype(i_c)::value;
+      pv(std::integral_constant<int, I>{});
+      expo(std::integral_constant<int, I + 1>{});
+      // 10 MFMAs, each followed by four of the 40 VALU instructions.
+#pragma unroll
+      for (int g = 0; g < 10; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) o[mb][DB] = Mfma16<T>::run(vf0, pf[mb][0], o[mb][DB]);
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) o[mb][DB] = Mfma16<T>::run(vf1, pf[mb][1], o[mb][DB]);
-      __builtin_amdgcn_sched_barrier(0);
-      if constexpr (DB < 3) {
-        vf0 = nv0;
-        vf1 = nv1;
-      }
     });
+    pv(std::integral_constant<int, 3>{});
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   uint16_t* Ob = static_cast<uint16_t*>(p.O) + b * p.sO + h * p.hO;

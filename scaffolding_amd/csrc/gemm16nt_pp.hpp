@@ -91,6 +91,17 @@ __device__ __forceinline__ u32x2 ds_read_tr16(uint32_t addr) {
   return v;
 }
 
+// Orders a wave's LDS writes before its later LDS reads of other lanes'
+// data (and the reads before later writes).  A wave's LDS instructions
+// execute in issue order, so this only has to stop the compiler from
+// moving accesses across it; no workgroup barrier is needed for data that
+// never leaves the wave.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
@@ -424,7 +435,13 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
   for (int ps = 0; ps < WM / ROWS_S; ++ps) {
-    __syncthreads();
+    // The staging region is private to this wave: only the first pass
+    // waits for the other waves (their last fragment reads of the main loop
+    // may touch it); later passes order this wave's own LDS accesses.
+    if (ps == 0)
+      __syncthreads();
+    else
+      wave_lds_sync();
 #pragma unroll
     for (int jj = 0; jj < ROWS_S / 16; ++jj) {
       const int j = ps * (ROWS_S / 16) + jj;
@@ -448,14 +465,20 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
         *reinterpret_cast<u32x2*>(stage + r * PITCH + (i * 16 + 4 * (lane >> 4)) * 2) = u32x2{lo, hi};
       }
     }
-    __syncthreads();
+    wave_lds_sync();
+    // All of this pass's staged row segments are read first (one LDS wait),
+    // then stored.
+    u32x4 vals[ROWS_S / ROWS_I];
+    const int cl = lane % LANES_ROW;
+#pragma unroll
+    for (int rr = 0; rr < ROWS_S / ROWS_I; ++rr)
+      vals[rr] = *reinterpret_cast<const u32x4*>(stage + (rr * ROWS_I + lane / LANES_ROW) * PITCH + cl * 16);
 #pragma unroll
     for (int rr = 0; rr < ROWS_S / ROWS_I; ++rr) {
       const int r = rr * ROWS_I + lane / LANES_ROW;
-      const int cl = lane % LANES_ROW;
       const int gm = m0 + wm * WM + ps * ROWS_S + r;
       const int gn = n0 + wn * WN + cl * 8;
-      const u32x4 val = *reinterpret_cast<const u32x4*>(stage + r * PITCH + cl * 16);
+      const u32x4 val = vals[rr];
       if (gm < M) {
         uint16_t* crow = C + (int64_t)gm * p.ldc;
         if (vec_ok && gn + 8 <= N) {
