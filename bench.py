@@ -5,11 +5,16 @@ Headline (``value``): the north-star workload of BASELINE.json — bf16
 ``linear_forward`` (GEMM + bias epilogue, fp32 accumulate) at
 M = N = K = 4096 — in TFLOP/s.  A "step" is one ``dev_linear_forward``
 launch over one resident 4096 x 4096 activation; K steps are timed with HIP
-events on the launch stream, bracketed by device synchronisation.
+events on the launch stream, bracketed by device synchronisation.  Every
+warm-up runs at least W steps and at least SETTLE_MS of device work: after
+idle the chip spends its first ~30 ms of load at a lower clock, so a short
+warm-up would time that transient instead of the sustained rate.  The JSON
+line reports the warm-up as run and the rate of its first steps.
 
 ``sweep`` times every other config of BASELINE.json the same way (C1 fp32
 Linear, C2 fp32 square matmul, C3 bf16 Linear+bias+SiLU at M = 1 / 16 /
-4096, C4 fp16 attention QK^T / softmax / PV, C5 bf16 DiT projections), with
+4096, C4 fp16 attention QK^T / softmax / PV, C5 bf16 DiT projections, their
+backward GEMMs, and the DiT block glue at C5's shape), with
 TFLOP/s or HBM GB/s and the roofline fraction.  HBM-bound skinny rows rotate
 four weight copies (> the 256 MB Infinity Cache) across steps.
 
@@ -40,6 +45,7 @@ PEAK_BF16 = 2.5e15      # dense bf16/fp16 MFMA, FLOP/s
 PEAK_FP32 = 157.3e12    # fp32 matrix, FLOP/s
 PEAK_HBM = 8.0e12       # HBM3E, B/s
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gemm16nt_pp_linear_4096.txt")
+SETTLE_MS = 100.0       # minimum device work in every warm-up (see Dev.time_steps)
 
 
 def log(*a):
@@ -60,19 +66,52 @@ class Dev:
         a = (self.rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
         return self.cu.gputensor_from_numpy(a, 0, dtype)
 
-    def time_steps(self, fn, steps, warmup):
+    def time_steps(self, fn, steps, warmup, info=None):
         """Mean ms per call of fn over `steps` calls enqueued back to back
-        between two events (after `warmup` calls and a device sync)."""
+        between two events, after the warm-up: at least `warmup` calls and
+        at least SETTLE_MS of device work.  The chip needs that long under
+        load to leave its power-management transient (measured: the first
+        ~100 launches of the 4096^3 GEMM after idle take 0.110 ms, then the
+        clock recovers and holds 0.0965 ms for thousands of launches), so
+        the timed region measures the sustained rate.  `info` (a dict)
+        receives the warm-up's own figures, the transient included."""
         cu = self.cu
         keep = []
-        # The warm-up keeps the same window of live outputs as the timed
-        # loop, so the caching allocator already holds every block the timed
-        # loop needs (no device allocation inside the timed region).
-        for i in range(max(warmup, 9)):
+
+        def call(i):
             keep.append(fn(i))
             if len(keep) > 8:
                 keep.pop(0)
+        # The warm-up keeps the same window of live outputs as the timed
+        # loop, so the caching allocator already holds every block the timed
+        # loop needs (no device allocation inside the timed region).
+        n0 = max(warmup, 9)
+        w0, w1 = cu.CudaEvent(), cu.CudaEvent()
         cu.device_synchronize()
+        w0.record()
+        for i in range(n0):
+            call(i)
+        w1.record()
+        w1.synchronize()
+        first_ms = w0.elapsed_time(w1)
+        # More warm-up in chunks of about 20 ms of device work, each sized
+        # from the rate of the chunk before, until SETTLE_MS have run.
+        per = max(first_ms / n0, 1e-3)
+        settle_ms, extra = 0.0, 0
+        while first_ms + settle_ms < SETTLE_MS:
+            chunk = max(1, min(int(np.ceil((SETTLE_MS - first_ms - settle_ms) / per)), int(20.0 / per) + 1))
+            w0.record()
+            for i in range(chunk):
+                call(n0 + extra + i)
+            w1.record()
+            w1.synchronize()
+            t = w0.elapsed_time(w1)
+            settle_ms += t
+            extra += chunk
+            per = max(t / chunk, 1e-3)
+        if info is not None:
+            info.update({"warmup_steps_run": n0 + extra, "warmup_ms": round(first_ms + settle_ms, 2),
+                         "first_steps": n0, "first_ms_per_step": round(first_ms / n0, 5)})
         e0, e1 = cu.CudaEvent(), cu.CudaEvent()
         e0.record()
         e0.synchronize()
@@ -82,14 +121,10 @@ class Dev:
             # GPU is busy when it records and host-side launch latency does
             # not open an idle gap inside the timed region.
             for i in range(4):
-                keep.append(fn(i))
-                if len(keep) > 8:
-                    keep.pop(0)
+                call(i)
             e0.record()
             for i in range(steps):
-                keep.append(fn(i))
-                if len(keep) > 8:
-                    keep.pop(0)
+                call(i)
             e1.record()
             e1.synchronize()
         finally:
@@ -106,9 +141,10 @@ def headline(d: Dev, steps: int, warmup: int):
     b = d.rand((n,), 0.01, "bfloat16")
     kern = cu.gemm_plan(1, m, n, k, 1, x.data_ptr, k, 0, w.data_ptr, k, 0, n, 0, x.dtype,
                         epi=1, ptr_bias=b.data_ptr)
-    ms = d.time_steps(lambda i: cu.dev_linear_forward(x, w, b), steps, warmup)
+    info = {}
+    ms = d.time_steps(lambda i: cu.dev_linear_forward(x, w, b), steps, warmup, info)
     flops = 2.0 * m * n * k
-    return {"ms": ms, "flops": flops, "kernel": kern, "m": m, "n": n, "k": k,
+    return {"ms": ms, "flops": flops, "kernel": kern, "m": m, "n": n, "k": k, "warmup_info": info,
             "bytes": float((m * k + n * k + m * n) * 2 + n * 2)}
 
 
@@ -353,10 +389,34 @@ def read_traffic():
     return None
 
 
+def trace_summary(path: str, last: int) -> None:
+    """Markdown summary of a rocprofv3 kernel-trace CSV: per kernel, every
+    dispatch, and for the most launched kernel also its last `last`
+    dispatches (the timed region of a bench.py run, whose warm-up comes
+    first)."""
+    import csv
+    rows = list(csv.DictReader(open(path)))
+    per = {}
+    for r in rows:
+        name = r["Kernel_Name"]
+        per.setdefault(name, []).append((int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    total = sum(e - b for v in per.values() for b, e in v)
+    print("| kernel | calls | avg µs | min µs | max µs | total µs | % |\n|---|---|---|---|---|---|---|")
+    for name, v in sorted(per.items(), key=lambda kv: -sum(e - b for b, e in kv[1])):
+        d = [(e - b) / 1e3 for b, e in v]
+        print("| `%s` | %d | %.2f | %.2f | %.2f | %.1f | %.2f |" % (
+            name[:110], len(d), sum(d) / len(d), min(d), max(d), sum(d), 100.0 * sum(d) * 1e3 / total))
+    name, v = max(per.items(), key=lambda kv: len(kv[1]))
+    v.sort()
+    d = [(e - b) / 1e3 for b, e in v[-last:]]
+    print("\nlast %d dispatches of `%s`: avg %.2f µs, min %.2f, max %.2f" % (
+        len(d), name[:110], sum(d) / len(d), min(d), max(d)))
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -365,7 +425,13 @@ def main(argv=None):
                     help="first run one fp32 x*1.0 pass over 1 GiB (reads 1 GiB, writes 1 GiB): the "
                          "known-traffic kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--no-headline", action="store_true")
+    ap.add_argument("--trace-summary", default=None, metavar="CSV",
+                    help="print a markdown summary of a rocprofv3 kernel-trace CSV (the last --steps "
+                         "dispatches of the most launched kernel separately) and exit; no GPU use")
     args = ap.parse_args(argv)
+    if args.trace_summary:
+        trace_summary(args.trace_summary, args.steps)
+        return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py: this build runs on one GPU only (the matmul hot path's kernels at one "
@@ -401,6 +467,9 @@ def main(argv=None):
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(h["ms"], 5),
+        # the warm-up as run: at least `warmup` steps and SETTLE_MS of device
+        # work; first_ms_per_step is the rate of the first steps after idle
+        "warmup_run": h["warmup_info"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
