@@ -54,19 +54,52 @@ __device__ __forceinline__ void norm_tail8(const NormParams& p, int64_t row, int
 // beta and modulation rows).  Mean, then the mean squared deviation from
 // the registers (two-pass: no cancellation), then the output.
 // RMS = true: no centring, rstd from the mean square, gamma only.
+// When the workgroup's four rows share one modulation group, its threads
+// first fold gamma, beta and the group's (scale, shift) into fp32
+// A = gamma (1 + scale), B = beta (1 + scale) + shift in LDS, while the
+// waves' row loads are in flight: one L2 read of the four vectors per
+// workgroup instead of one per row, off the rows' critical path.
 template <typename T, int CPL, bool RMS>
 __global__ __launch_bounds__(256) void norm_wave_kernel(NormParams p) {
+  __shared__ __attribute__((aligned(16))) float sAB[2][CPL * 512];
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= p.rows) return;
+  const int64_t row_first = (int64_t)blockIdx.x * 4;
+  const int64_t row_last = (row_first + 3 < p.rows ? row_first + 3 : p.rows - 1);
+  const bool folded = !RMS && row_first / p.group_rows == row_last / p.group_rows;  // workgroup-uniform
   const int nch = p.cols >> 3;
+  if (folded) {
+    const int64_t moff = (row_first / p.group_rows) * p.mld;
+    for (int ch = threadIdx.x; ch < nch; ch += 256) {
+      float gm[8], bt[8], sc[8], sh[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { gm[e] = 1.f; bt[e] = 0.f; sc[e] = 0.f; sh[e] = 0.f; }
+      if (p.gamma) Chunk8<T>::load(p.gamma, ch * 8, gm);
+      if (p.beta) Chunk8<T>::load(p.beta, ch * 8, bt);
+      if (p.mscale) Chunk8<T>::load(p.mscale, moff + ch * 8, sc);
+      if (p.mshift) Chunk8<T>::load(p.mshift, moff + ch * 8, sh);
+      f32x4 a0, a1, b0, b1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        a0[e] = gm[e] * (1.0f + sc[e]);
+        a1[e] = gm[e + 4] * (1.0f + sc[e + 4]);
+        b0[e] = bt[e] * (1.0f + sc[e]) + sh[e];
+        b1[e] = bt[e + 4] * (1.0f + sc[e + 4]) + sh[e + 4];
+      }
+      *reinterpret_cast<f32x4*>(&sAB[0][ch * 8]) = a0;
+      *reinterpret_cast<f32x4*>(&sAB[0][ch * 8 + 4]) = a1;
+      *reinterpret_cast<f32x4*>(&sAB[1][ch * 8]) = b0;
+      *reinterpret_cast<f32x4*>(&sAB[1][ch * 8 + 4]) = b1;
+    }
+  }
+  const bool live = row < p.rows;
   const int64_t base = row * p.cols;
   float v[CPL][8];
   float sum = 0.f;
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
     const int ch = c * 64 + lane;
-    if (ch < nch) {
+    if (live && ch < nch) {
       Chunk8<T>::load(p.x, base + ch * 8, v[c]);
       if constexpr (!RMS) {
 #pragma unroll
@@ -74,6 +107,8 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(NormParams p) {
       }
     }
   }
+  if (folded) __syncthreads();  // the folded coefficients are in LDS
+  if (!live) return;
   const float inv_n = 1.0f / (float)p.cols;
   float mu = 0.f;
   if constexpr (!RMS) mu = wave_sum(sum) * inv_n;
@@ -102,6 +137,16 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(NormParams p) {
           Chunk8<T>::load(p.gamma, ch * 8, g);
 #pragma unroll
           for (int e = 0; e < 8; ++e) v[c][e] *= g[e];
+        }
+      } else if (folded) {
+        const f32x4 a0 = *reinterpret_cast<const f32x4*>(&sAB[0][ch * 8]);
+        const f32x4 a1 = *reinterpret_cast<const f32x4*>(&sAB[0][ch * 8 + 4]);
+        const f32x4 b0 = *reinterpret_cast<const f32x4*>(&sAB[1][ch * 8]);
+        const f32x4 b1 = *reinterpret_cast<const f32x4*>(&sAB[1][ch * 8 + 4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[c][e] = v[c][e] * a0[e] + b0[e];
+          v[c][e + 4] = v[c][e + 4] * a1[e] + b1[e];
         }
       } else {
         norm_tail8<T, true>(p, row, ch * 8, v[c]);
@@ -206,7 +251,10 @@ int launch_norm(const NormArgs& a, sf_dtype dt, hipStream_t st) {
   p.mscale = a.mscale; p.mshift = a.mshift;
   p.mean_out = a.mean_out; p.rstd_out = a.rstd_out;
   p.rows = a.rows; p.cols = (int)a.cols; p.eps = a.eps;
-  p.mld = a.mld; p.group_rows = a.group_rows > 0 ? a.group_rows : 1;
+  // Without modulation every row shares one set of coefficients (group 0).
+  const bool mod = a.mscale != nullptr || a.mshift != nullptr;
+  p.mld = a.mld;
+  p.group_rows = mod ? (a.group_rows > 0 ? a.group_rows : 1) : (a.rows > 0 ? a.rows : 1);
   const int per16 = dt == SF_F32 ? 4 : 8;
   // The register-resident kernel loads 8-element chunks (16 or 32 bytes):
   // every row it touches must start 16-byte aligned.
