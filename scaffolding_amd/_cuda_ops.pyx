@@ -986,6 +986,10 @@ def dev_add(gt_a, gt_b):
     return out
 
 
+# Score memory of the unfused multi-head fallback per launch group.
+_MHA_SCORES_BYTES = 1 << 30
+
+
 cdef object _mha_strided(q, int64_t q_off, int64_t ldq, k, int64_t k_off, int64_t ldk,
                          v, int64_t v_off, int64_t ldv, int64_t B, int64_t Nq, int64_t Sk,
                          int64_t H, int64_t D, float scale):
@@ -1008,25 +1012,35 @@ cdef object _mha_strided(q, int64_t q_off, int64_t ldq, k, int64_t k_off, int64_
         if ret != SF_ERR_UNSUPPORTED:
             _check_kernel(ret)
             return out
-    # Any head size, dtype or scale: per batch entry, scores of all heads by
-    # one strided-batched NT GEMM (the scale in its epilogue), the row
-    # softmax, then one strided-batched NN GEMM writing the heads side by
-    # side into the output rows.
-    scores = _alloc_like((H, Nq, Sk), dt, q.device_id)
+    # Any head size, dtype or scale: per batch entry and group of heads,
+    # the scores of those heads by one strided-batched NT GEMM (the scale in
+    # its epilogue), the row softmax, then one strided-batched NN GEMM
+    # writing the heads side by side into the output rows.  A head group's
+    # scores stay within _MHA_SCORES_BYTES (at least one head).
+    cdef int64_t per_head = Nq * Sk * es
+    cdef int64_t hg = _MHA_SCORES_BYTES // per_head if per_head > 0 else H
+    if hg < 1:
+        hg = 1
+    if hg > H:
+        hg = H
+    scores = _alloc_like((hg, Nq, Sk), dt, q.device_id)
     cdef char* ps = <char*>_ptr(scores)
-    cdef int64_t b
+    cdef int64_t b, h0, nh
     for b in range(B):
-        with nogil:
-            ret = sf_gemm(0, 1, Nq, Sk, D, H, pq + b * Nq * ldq * es, ldq, D, pk + b * Sk * ldk * es, ldk, D,
-                          ps, Sk, Nq * Sk, sdt, sdt, scale, NULL, SF_EPI_NONE, NULL)
-        _check_kernel(ret)
-        with nogil:
-            ret = sf_softmax_rows(ps, ps, H * Nq, Sk, sdt, sdt, 1.0, NULL)
-        _check_kernel(ret)
-        with nogil:
-            ret = sf_gemm(0, 0, Nq, D, Sk, H, ps, Sk, Nq * Sk, pv + b * Sk * ldv * es, ldv, D,
-                          po + b * Nq * C * es, C, D, sdt, sdt, 1.0, NULL, SF_EPI_NONE, NULL)
-        _check_kernel(ret)
+        for h0 in range(0, H, hg):
+            nh = H - h0 if H - h0 < hg else hg
+            with nogil:
+                ret = sf_gemm(0, 1, Nq, Sk, D, nh, pq + (b * Nq * ldq + h0 * D) * es, ldq, D,
+                              pk + (b * Sk * ldk + h0 * D) * es, ldk, D,
+                              ps, Sk, Nq * Sk, sdt, sdt, scale, NULL, SF_EPI_NONE, NULL)
+            _check_kernel(ret)
+            with nogil:
+                ret = sf_softmax_rows(ps, ps, nh * Nq, Sk, sdt, sdt, 1.0, NULL)
+            _check_kernel(ret)
+            with nogil:
+                ret = sf_gemm(0, 0, Nq, D, Sk, nh, ps, Sk, Nq * Sk, pv + (b * Sk * ldv + h0 * D) * es, ldv, D,
+                              po + (b * Nq * C + h0 * D) * es, C, D, sdt, sdt, 1.0, NULL, SF_EPI_NONE, NULL)
+            _check_kernel(ret)
     return out
 
 

@@ -151,7 +151,10 @@ static int choose_tile32(int64_t M, int64_t N, int64_t batch, bool vec, int cus)
 // so the buffer is ready for the next launch.  Launches on one stream are
 // ordered by the stream; a launch on another stream first waits for the
 // event recorded after the previous split launch.  Growing the buffer
-// synchronises the device before freeing the old one.
+// synchronises the device before freeing the old one.  The lock is held
+// from split_workspace_acquire to split_workspace_release, so calls from
+// several host threads enqueue their workspace launches one at a time and
+// each one's event wait sees the previous one's record.
 // ---------------------------------------------------------------------
 struct SplitWorkspace {
   void* base = nullptr;
@@ -164,11 +167,25 @@ struct SplitWorkspace {
 static std::mutex g_ws_mu;
 static std::unordered_map<int, SplitWorkspace> g_ws;
 
+static int split_workspace_acquire_locked(int dev, size_t part_bytes, int ncounters, hipStream_t st, float** ws,
+                                          int** cnt);
+
+// On SF_OK the workspace lock stays held until split_workspace_release,
+// which the caller must then call (after its launch, whatever that
+// returned); on failure nothing stays locked.
 static int split_workspace_acquire(size_t part_bytes, int ncounters, hipStream_t st, float** ws, int** cnt) {
   int dev = 0;
   int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
   if (rc != SF_OK) return rc;
-  std::lock_guard<std::mutex> lk(g_ws_mu);
+  g_ws_mu.lock();
+  rc = split_workspace_acquire_locked(dev, part_bytes, ncounters, st, ws, cnt);
+  if (rc != SF_OK) g_ws_mu.unlock();
+  return rc;
+}
+
+static int split_workspace_acquire_locked(int dev, size_t part_bytes, int ncounters, hipStream_t st, float** ws,
+                                          int** cnt) {
+  int rc = SF_OK;
   SplitWorkspace& w = g_ws[dev];
   if (w.done == nullptr) {
     rc = check_hip(hipEventCreateWithFlags(&w.done, hipEventDisableTiming), "hipEventCreate (split workspace)");
@@ -206,11 +223,13 @@ static int split_workspace_acquire(size_t part_bytes, int ncounters, hipStream_t
   return SF_OK;
 }
 
+// Records the event after the caller's launch and releases the lock taken
+// by split_workspace_acquire.
 static int split_workspace_release(hipStream_t st) {
+  std::lock_guard<std::mutex> lk(g_ws_mu, std::adopt_lock);
   int dev = 0;
   int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
   if (rc != SF_OK) return rc;
-  std::lock_guard<std::mutex> lk(g_ws_mu);
   SplitWorkspace& w = g_ws[dev];
   w.last = st;
   w.used = true;

@@ -370,3 +370,80 @@ def test_dit_block_state_dict_roundtrip_and_keys():
     assert other.to_qkv.weight is w_before          # updated in place
     for k, v in blk.state_dict().items():
         assert np.array_equal(other.state_dict()[k].numpy(), v.numpy()), k
+
+
+def test_multihead_fallback_head_groups_match():
+    """The unfused path launches heads in groups that bound its score
+    memory; one head per group and all heads at once give the same bits."""
+    g = cu()
+    rng = np.random.default_rng(44)
+    q, k, v = (rnd(rng, (2, 30, 5 * 40), 1.0, "bfloat16") for _ in range(3))
+    gq, gk, gv = up(q, "bfloat16"), up(k, "bfloat16"), up(v, "bfloat16")
+    whole = down(g.dev_multihead_attention(gq, gk, gv, 5))
+    saved = g._MHA_SCORES_BYTES
+    try:
+        g._MHA_SCORES_BYTES = 1
+        one_by_one = down(g.dev_multihead_attention(gq, gk, gv, 5))
+        g._MHA_SCORES_BYTES = 2 * 30 * 30 * 2
+        pairs = down(g.dev_multihead_attention(gq, gk, gv, 5))
+    finally:
+        g._MHA_SCORES_BYTES = saved
+    assert np.array_equal(whole, one_by_one) and np.array_equal(whole, pairs)
+    o64 = dit.mha_f64(q, k, v, 5)
+    assert float(np.max(np.abs(whole - o64))) <= 0.05
+
+
+def test_split_workspace_two_threads_two_streams():
+    """Split-tail GEMMs from two host threads on two streams share the
+    per-device workspace: its lock spans each launch, so every result equals
+    the single-threaded one bit for bit and the counters stay consistent."""
+    import threading
+    so = _lib()
+    g = cu()
+    P, I64 = ctypes.c_void_p, ctypes.c_int64
+    rng = np.random.default_rng(3)
+    m, n, k = 4352, 4096, 256
+    plan = g.gemm_plan(1, m, n, k, 1, 4096, k, 0, 8192, k, 0, n, m * n, "bfloat16")
+    assert "split-tail" in plan, plan
+    xs = [up(rnd(rng, (m, k), 1.0, "bfloat16"), "bfloat16") for _ in range(2)]
+    w = up(rnd(rng, (n, k), 0.05, "bfloat16"), "bfloat16")
+    outs = [g.empty((m, n), g.BFLOAT16) for _ in range(2)]
+    g.device_synchronize()  # the uploads' casts ran on the default stream
+    streams = []
+    for _ in range(2):
+        sp = ctypes.c_void_p()
+        assert so.sf_stream_create(ctypes.byref(sp)) == 0
+        streams.append(sp)
+
+    def gemm(i, stream):
+        return so.sf_gemm(0, 1, I64(m), I64(n), I64(k), I64(1), P(xs[i].data_ptr), I64(k), I64(0),
+                          P(w.data_ptr), I64(k), I64(0), P(outs[i].data_ptr), I64(n), I64(0), 2, 2,
+                          ctypes.c_float(1.0), None, 0, stream)
+    want = []
+    for i in range(2):
+        assert gemm(i, streams[i]) == 0
+        assert so.sf_stream_synchronize(streams[i]) == 0
+        want.append(g.gputensor_bits_to_numpy(outs[i]).copy())
+    errors = []
+
+    def worker(i):
+        for _ in range(40):
+            rc = gemm(i, streams[i])
+            if rc != 0:
+                errors.append(rc)
+                return
+        so.sf_stream_synchronize(streams[i])
+
+    ts = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errors
+    for i in range(2):
+        assert np.array_equal(g.gputensor_bits_to_numpy(outs[i]), want[i])
+    # and a later call is still right (the counters were left at zero)
+    assert gemm(0, streams[0]) == 0 and so.sf_stream_synchronize(streams[0]) == 0
+    assert np.array_equal(g.gputensor_bits_to_numpy(outs[0]), want[0])
+    for sp in streams:
+        so.sf_stream_destroy(sp)
