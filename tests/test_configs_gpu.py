@@ -12,6 +12,9 @@ properties over every element (row / column checksums for the linear maps,
 row sums of the softmax)."""
 from __future__ import annotations
 
+import json
+import os
+
 import numpy as np
 import pytest
 
@@ -20,6 +23,24 @@ from oracle import configs as cfg
 from oracle import cpu_path as ref
 
 pytestmark = pytest.mark.gpu
+
+# Each check's measured error against its gate; written as JSON to the path
+# in SF_PARITY_REPORT (if set) when the module's tests end.
+_REPORT = []
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _parity_report():
+    yield
+    path = os.environ.get("SF_PARITY_REPORT")
+    if path and _REPORT:
+        with open(path, "w") as f:
+            json.dump(_REPORT, f, indent=1)
+
+
+def _gate(check: str, err: float, tol: float) -> float:
+    _REPORT.append({"check": check, "max_err": float(err), "tol": float(tol)})
+    return err
 
 
 def _plan_linear(gx, gw, gb, m, n, k):
@@ -34,7 +55,7 @@ def test_c1_linear_fp32():
     assert gy.shape == (64, 512) and gy.dtype == np.float32
     y = down(gy)
     y_cpu = ref.linear(case.x, case.w, case.b)
-    err = cfg.normwise_err(y, y_cpu)
+    err = _gate("C1 fp32 linear, normwise vs CPU fp32", cfg.normwise_err(y, y_cpu), cfg.tol_fp32(512))
     assert err <= cfg.tol_fp32(512), err
     # and against the exact value
     assert cfg.normwise_err(y, ref.linear_f64(case.x, case.w, case.b)) <= cfg.tol_fp32(512)
@@ -48,7 +69,8 @@ def test_c2_matmul_fp32(n):
     assert y.shape == (n, n)
     rows = sample_rows(n, 192, seed=n, tile=128)
     y_cpu = ref.matmul(a[rows], b)  # the reference CPU path on these rows
-    err = cfg.normwise_err(y[rows], y_cpu)
+    err = _gate("C2 fp32 matmul %d, normwise vs CPU fp32 (sampled rows)" % n, cfg.normwise_err(y[rows], y_cpu),
+                cfg.tol_fp32(n))
     assert err <= cfg.tol_fp32(n), err
     # every row and column: checksums against fp64
     a64, b64 = a.astype(np.float64), b.astype(np.float64)
@@ -73,7 +95,7 @@ def test_c3_linear_silu_bf16(m):
     y = down(gy)
     rows = np.arange(m) if m <= 16 else sample_rows(m, 256, seed=2)
     y64 = ref.linear_f64(case.x[rows], case.w, case.b, "silu")
-    err = cfg.abs_err(y[rows], y64)
+    err = _gate("C3 bf16 linear+bias+SiLU M=%d, abs vs fp64" % m, cfg.abs_err(y[rows], y64), cfg.tol_16(k))
     assert err <= cfg.tol_16(k), err
     assert np.all(np.isfinite(y))
 
@@ -92,7 +114,8 @@ def test_c4_attention_fp16():
     rows = sample_rows(s, 24, seed=34)
     for h in heads:
         s64 = scale * (q[h, rows].astype(np.float64) @ k[h].astype(np.float64).T)
-        err = cfg.abs_err(scores[h, rows].astype(np.float32), s64)
+        err = _gate("C4 fp16 alpha-scaled QK^T head %d, abs vs fp64" % h,
+                    cfg.abs_err(scores[h, rows].astype(np.float32), s64), cfg.tol_16(d))
         assert err <= cfg.tol_16(d), (h, err)
     # softmax over every row: rows sum to one (fp16 output spacing bound)
     gp = g.dev_softmax(gs, -1)
@@ -110,7 +133,8 @@ def test_c4_attention_fp16():
         del go
         for h in heads:
             o64 = ref.sdpa_f64(q[h:h + 1, rows], k[h:h + 1], v[h:h + 1], scale)[0]
-            err = cfg.abs_err(o[h, rows], o64)
+            err = _gate("C4 fp16 SDPA (%s) head %d, abs vs fp64" % (fn.__name__, h), cfg.abs_err(o[h, rows], o64),
+                        cfg.tol_16(s))
             assert err <= cfg.tol_16(s), (fn.__name__, h, err)
 
 
@@ -127,7 +151,7 @@ def test_c5_dit_projections_bf16(proj):
     y = down(gy)
     rows = sample_rows(m, 192, seed=4 + k + n)
     y64 = ref.linear_f64(case.x[rows], case.w, case.b, case.act)
-    err = cfg.abs_err(y[rows], y64)
+    err = _gate("C5 bf16 %s, abs vs fp64 (sampled rows)" % proj, cfg.abs_err(y[rows], y64), cfg.tol_16(k))
     assert err <= cfg.tol_16(k), err
     if case.act is None:
         # every row: y . 1 = x . (W^T 1) + sum(b), fp64 on the quantized inputs
