@@ -348,31 +348,27 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- split tile: park the partial, the last part sums all of them ---------
-  // Partials move with agent-scope coherent stores (sc0 sc1, 16 bytes) and
-  // relaxed agent-scope atomic loads: coherent across the XCDs' separate L2s
-  // without the whole-L2 writeback and invalidate a device-scope fence costs.  Each thread waits for its own stores to
-  // complete (vmcnt 0) before the workgroup barrier that precedes the
-  // counter increment, so the part that sees count split - 1 reads every
-  // other part's data from memory.
+  // Partials move with plain 16-byte stores and loads.  Each thread waits
+  // for its own stores (vmcnt 0) before the workgroup barrier; the counter
+  // increment after it is an agent-scope release and acquire
+  // (split_arrive), so the part that sees count split - 1 reads every other
+  // part's data as written.
   if (NSTAGE == 2 && part >= 0) {
     const int tid = threadIdx.x;
     float* mine = p.ws + (size_t)(split_tile * p.split + part) * (FN * FM * 512 * 4);
-    mfma_drain();
 #pragma unroll
     for (int i = 0; i < FN; ++i)
 #pragma unroll
       for (int j = 0; j < FM; ++j)
-        store16_coherent(mine + (size_t)((i * FM + j) * 512 + tid) * 4, acc[i][j]);
+        *reinterpret_cast<f32x4*>(mine + (size_t)((i * FM + j) * 512 + tid) * 4) = acc[i][j];
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     __shared__ int arrived;
-    if (tid == 0)
-      arrived = __hip_atomic_fetch_add(&p.counters[split_tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) arrived = split_arrive(&p.counters[split_tile], p.split);
     __syncthreads();
     if (arrived != p.split - 1) return;  // workgroup-uniform
     // Sum the parts in part order (the same bits whichever part is last),
-    // one B block (8 fragments, 8 coherent 16-byte loads in flight) per
-    // round trip.
+    // one B block (8 fragments, 8 16-byte loads in flight) per round trip.
     const float* all = p.ws + (size_t)split_tile * p.split * (FN * FM * 512 * 4);
 #pragma unroll
     for (int i = 0; i < FN; ++i) {
@@ -385,8 +381,7 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
         const float* src = all + ((size_t)q * (FN * FM) + i * FM) * 512 * 4 + (size_t)tid * 4;
         f32x4 v[FM];
 #pragma unroll
-        for (int j = 0; j < FM; ++j) v[j] = load16_coherent_nowait(src + (size_t)j * 512 * 4);
-        wait_vm0_tie8(v);
+        for (int j = 0; j < FM; ++j) v[j] = *reinterpret_cast<const f32x4*>(src + (size_t)j * 512 * 4);
 #pragma unroll
         for (int j = 0; j < FM; ++j) sum[j] += v[j];
       }

@@ -201,20 +201,19 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm32_kernel(GemmParam
 
   // ---- split-K: park the partial, the last part sums all of them in part
   // order (the same protocol as the 16-bit LDS-DMA kernel's split tail:
-  // coherent stores, a relaxed agent-scope counter, coherent loads).
+  // plain stores, the counter bumped by split_arrive, plain loads).
   if (part >= 0) {
     constexpr int NF = FN * FM;
     float* mine = p.ws + (size_t)(tile_id * p.split + part) * (NF * NT * 4);
-    mfma_drain();
 #pragma unroll
     for (int i = 0; i < FN; ++i)
 #pragma unroll
-      for (int j = 0; j < FM; ++j) store16_coherent(mine + (size_t)((i * FM + j) * NT + tid) * 4, acc[i][j]);
+      for (int j = 0; j < FM; ++j)
+        *reinterpret_cast<f32x4*>(mine + (size_t)((i * FM + j) * NT + tid) * 4) = acc[i][j];
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     __shared__ int arrived;
-    if (tid == 0)
-      arrived = __hip_atomic_fetch_add(&p.counters[tile_id], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) arrived = split_arrive(&p.counters[tile_id], p.split);
     __syncthreads();
     if (arrived != p.split - 1) return;  // workgroup-uniform
     const float* all = p.ws + (size_t)tile_id * p.split * (NF * NT * 4);
@@ -230,8 +229,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm32_kernel(GemmParam
         const float* src = all + ((size_t)q * NF + 4 * c) * NT * 4 + (size_t)tid * 4;
         f32x4 v[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = load16_coherent_nowait(src + (size_t)u * NT * 4);
-        wait_vm0_tie4(v);
+        for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const f32x4*>(src + (size_t)u * NT * 4);
 #pragma unroll
         for (int u = 0; u < 4; ++u) sum[u] += v[u];
       }
