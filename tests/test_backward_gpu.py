@@ -194,8 +194,8 @@ LDS_DMA_CASES = [
     ("bfloat16", 1, 1, 4096, 4096, 128, 1, 0, "gemm tt 256x256 lds-dma"),
     ("float16", 0, 0, 1000, 1104, 128, 16, 0, "gemm nn 256x256 lds-dma"),
     ("bfloat16", 1, 0, 1000, 1104, 256, 16, 0, "gemm tn 256x256 lds-dma"),
-    ("bfloat16", 1, 0, 4352, 4096, 1024, 1, 0, "gemm tn 256x256 lds-dma 16-bit split-tail 16x8"),
-    ("bfloat16", 0, 0, 4352, 4096, 1024, 1, 1, "gemm nn 256x256 lds-dma 16-bit split-tail 16x8"),
+    ("bfloat16", 1, 0, 4352, 4096, 4096, 1, 0, "gemm tn 256x256 lds-dma 16-bit split-tail 16x8"),
+    ("bfloat16", 0, 0, 4352, 4096, 4096, 1, 1, "gemm nn 256x256 lds-dma 16-bit split-tail 16x8"),
     ("bfloat16", 0, 0, 2104, 8000, 512, 1, 3, "gemm nn 256x256 lds-dma"),
     ("float16", 1, 0, 2104, 8000, 512, 1, 2, "gemm tn 256x256 lds-dma"),
     # weight-gradient shapes: few output tiles, long and ragged K (tokens)

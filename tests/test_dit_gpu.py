@@ -135,7 +135,7 @@ RES_CASES = [  # (dtype, m, n, k, kernel name prefix)
     ("float16", 70, 200, 136, "gemm tile"),
     ("bfloat16", 300, 520, 264, "gemm tile"),
     ("bfloat16", 4096, 4096, 128, "gemm nt 256x256 lds-dma"),
-    ("bfloat16", 4352, 4096, 256, "gemm nt 256x256 lds-dma"),  # split tail
+    ("bfloat16", 4352, 4096, 4096, "gemm nt 256x256 lds-dma"),  # split tail
     ("float32", 70, 200, 136, "gemm tile"),
     ("float32", 64, 64, 1024, "gemm tile"),                   # fp32 split-K
     ("float32", 5, 33, 20, "gemm"),
@@ -402,7 +402,7 @@ def test_split_workspace_two_threads_two_streams():
     g = cu()
     P, I64 = ctypes.c_void_p, ctypes.c_int64
     rng = np.random.default_rng(3)
-    m, n, k = 4352, 4096, 256
+    m, n, k = 4352, 4096, 4096
     plan = g.gemm_plan(1, m, n, k, 1, 4096, k, 0, 8192, k, 0, n, m * n, "bfloat16")
     assert "split-tail" in plan, plan
     xs = [up(rnd(rng, (m, k), 1.0, "bfloat16"), "bfloat16") for _ in range(2)]

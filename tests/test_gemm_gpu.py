@@ -262,9 +262,9 @@ def test_skinny_line_fp32_output():
 
 SPLIT_CASES = [
     # (M, N, K, act, bias, expected "split-tail R x s")
-    (4352, 4096, 1024, None, False, "split-tail 16x8"),    # 272 tiles: 16 left over, 8 parts of 128 k
-    (7900, 2800, 896, "gelu", True, "split-tail 85x3"),   # 341 tiles: 85 left, 7 units in 3 uneven parts
-    (17776, 1920, 1920, None, True, "split-tail 48x5"),   # C5 out-projection shape
+    (4352, 4096, 4096, None, False, "split-tail 16x8"),    # 272 tiles: 16 left over, 8 parts of 4 units
+    (7900, 2800, 4352, "gelu", True, "split-tail 85x3"),  # 341 tiles: 85 left, 34 units in 3 uneven parts
+    (17776, 1920, 7680, None, True, "split-tail 48x5"),   # C5 MLP-down shape
 ]
 
 
