@@ -149,9 +149,12 @@ static int choose_tile32(int64_t M, int64_t N, int64_t batch, bool vec, int cus)
 // counter per split tile.  Counters start at zero (cleared by a kernel when
 // the buffer is created) and every split tile's last part resets its own,
 // so the buffer is ready for the next launch.  Launches on one stream are
-// ordered by the stream; a launch on another stream first waits for the
-// event recorded after the previous split launch.  Growing the buffer
-// synchronises the device before freeing the old one.  The lock is held
+// ordered by the stream, and while every split launch has come on one
+// stream nothing else is done (an event record costs about 3 us of host
+// time per call).  The first split launch on a second stream synchronises
+// the device once; from then on an event is recorded after every split
+// launch and a launch on another stream first waits for it.  Growing the
+// buffer synchronises the device before freeing the old one.  The lock is held
 // from split_workspace_acquire to split_workspace_release, so calls from
 // several host threads enqueue their workspace launches one at a time and
 // each one's event wait sees the previous one's record.
@@ -163,6 +166,7 @@ struct SplitWorkspace {
   hipEvent_t done = nullptr;
   hipStream_t last = nullptr;
   bool used = false;
+  bool multi = false;  // split launches have come on more than one stream
 };
 static std::mutex g_ws_mu;
 static std::unordered_map<int, SplitWorkspace> g_ws;
@@ -215,7 +219,14 @@ static int split_workspace_acquire_locked(int dev, size_t part_bytes, int ncount
     w.counters = nc;
     w.used = false;
   } else if (w.used && w.last != st) {
-    rc = check_hip(hipStreamWaitEvent(st, w.done, 0), "hipStreamWaitEvent (split workspace)");
+    if (w.multi) {
+      rc = check_hip(hipStreamWaitEvent(st, w.done, 0), "hipStreamWaitEvent (split workspace)");
+    } else {
+      // No event was recorded after the earlier launches: wait for them
+      // once (safe even if their stream has been destroyed since).
+      rc = check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize (split workspace, second stream)");
+      w.multi = true;
+    }
     if (rc != SF_OK) return rc;
   }
   *ws = static_cast<float*>(w.base);
@@ -223,8 +234,9 @@ static int split_workspace_acquire_locked(int dev, size_t part_bytes, int ncount
   return SF_OK;
 }
 
-// Records the event after the caller's launch and releases the lock taken
-// by split_workspace_acquire.
+// Records the event after the caller's launch (once split launches have
+// come on more than one stream) and releases the lock taken by
+// split_workspace_acquire.
 static int split_workspace_release(hipStream_t st) {
   std::lock_guard<std::mutex> lk(g_ws_mu, std::adopt_lock);
   int dev = 0;
@@ -233,6 +245,7 @@ static int split_workspace_release(hipStream_t st) {
   SplitWorkspace& w = g_ws[dev];
   w.last = st;
   w.used = true;
+  if (!w.multi) return SF_OK;
   return check_hip(hipEventRecord(w.done, st), "hipEventRecord (split workspace)");
 }
 
