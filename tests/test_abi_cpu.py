@@ -110,6 +110,14 @@ def test_dispatch_for_config_shapes():
     assert plan().startswith("gemm nt 256x256 lds-dma")
     assert plan(M=4096, N=11008, ldc=11008).startswith("gemm nt 256x256 lds-dma")
     assert plan(M=17776, N=1920, K=7680, lda=7680, ldb=7680, ldc=1920).startswith("gemm nt 256x256 lds-dma")
+    # C5 tails (560 / 1610 / 2100 tiles): behind whole waves only K >= 4096
+    # splits the last wave (MLP-down); out-projection, QKV and MLP-up run it
+    # unsplit
+    assert plan(M=17776, N=1920, K=7680, lda=7680, ldb=7680, ldc=1920) \
+        == "gemm nt 256x256 lds-dma 16-bit split-tail 48x5"
+    assert plan(M=17776, N=1920, K=1920, lda=1920, ldb=1920, ldc=1920) == "gemm nt 256x256 lds-dma 16-bit"
+    assert plan(M=17776, N=5760, K=1920, lda=1920, ldb=1920, ldc=5760) == "gemm nt 256x256 lds-dma 16-bit"
+    assert plan(M=17776, N=7680, K=1920, lda=1920, ldb=1920, ldc=7680) == "gemm nt 256x256 lds-dma 16-bit"
     # C3 decode shapes -> row-segment stream kernel (K = 512 x waves)
     assert plan(M=1, N=11008, ldc=11008).startswith("gemm skinny line")
     assert plan(M=16, N=11008, ldc=11008).startswith("gemm skinny line")
