@@ -17,9 +17,9 @@
  * Reference interface this replaces (all /root/reference paths):
  *   _cuda_ops_decl.h:107-117   cuda_sgemm / cuda_sgemm_batched (cuBLAS)
  *   _cuda_ops_decl.h:136-137   cuda_bias_add_row_f32
- *   _cuda_ops_decl.h:63-72     cuda_silu_f32 / cuda_gelu_f32
- *   _cuda_ops_decl.h:59        cuda_muls_f32
- *   _cuda_ops_decl.h:78-79     cuda_softmax_f32
+ *   _cuda_ops_decl.h:69, :74   cuda_silu_f32 / cuda_gelu_f32
+ *   _cuda_ops_decl.h:63        cuda_muls_f32
+ *   _cuda_ops_decl.h:83-84     cuda_softmax_f32
  *   _cuda_ops.pyx:33-142       CUDA runtime calls the Cython module binds
  *                              directly (malloc/free/memcpy/device/stream/event)
  *   _cuda_ops.pyx:357-475      caching allocator (here native, in C++)
@@ -233,7 +233,7 @@ int sf_add(const void* a, const void* b, void* y, int64_t n, sf_dtype dt, void* 
 
 /* Row softmax: y[r,:] = softmax(scale * x[r,:]) for r in [0, rows).
  * Contiguous rows of `cols` elements.  Replaces cuda_softmax_f32
- * (_cuda_kernels.cu:473-640, decl _cuda_ops_decl.h:78-79) with the
+ * (_cuda_kernels.cu:473-640, decl _cuda_ops_decl.h:83-84) with the
  * dev_muls pre-scale of scaled_dot_product_attention
  * (nn/functional.py:315-316) folded in.  in/out dtypes independently
  * F32/F16/BF16; arithmetic is fp32. */

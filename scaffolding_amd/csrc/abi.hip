@@ -6,6 +6,7 @@
 // same way with or without a GPU.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -97,9 +98,16 @@ int launch_gemm16(sf_dtype in, sf_dtype out, bool a_kmajor, bool b_kmajor, int c
 static std::mutex g_props_mu;
 static std::unordered_map<int, int> g_cu_count;
 
+// Without a device (sf_gemm_plan on a host with no GPU) the planner assumes
+// 256 CUs, or the count in SF_PLAN_CU_COUNT, so the plans of other parts
+// can be checked on the host; a visible device always reports its own.
 static int cu_count_current() {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    const char* s = getenv("SF_PLAN_CU_COUNT");
+    const int v = s != nullptr ? atoi(s) : 0;
+    return v > 0 && v <= 4096 ? v : 256;
+  }
   std::lock_guard<std::mutex> lk(g_props_mu);
   auto it = g_cu_count.find(dev);
   if (it != g_cu_count.end()) return it->second;
@@ -429,9 +437,12 @@ static int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K,
     // parts' L2 write-back and partial sums cost more than a short tail
     // (M = 17776, N = 1920: K = 1920 runs 134 us unsplit against 148 us in
     // 5 parts; K = 7680 runs 467 us in 5 parts against 560 us unsplit).
+    // The kernel gives every XCD (T - R) / 8 whole tiles, so the split is
+    // taken only when the whole tiles divide evenly over the XCDs (always
+    // true while the CU count is a multiple of 8).
     const int64_t T = (int64_t)p.tiles_m * p.tiles_n, R = T % cus, units = (K + 127) / 128;
     const int64_t min_units = T > R ? 32 : 2;
-    if (R > 0 && 2 * R <= cus && units >= min_units) {
+    if (R > 0 && 2 * R <= cus && units >= min_units && (T - R) % kNumXcd == 0) {
       int64_t sp = cus / R;
       if (sp > units) sp = units;
       if (sp > 8) sp = 8;

@@ -84,13 +84,20 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
   const uint32_t vk0 = (uint32_t)drow * (uint32_t)p.ldk * 2u + dch;
   const uint32_t vv0 = (uint32_t)drow * (uint32_t)p.ldv * 2u + dch;
   const uint32_t k8 = 8u * (uint32_t)p.ldk * 2u, v8 = 8u * (uint32_t)p.ldv * 2u;
+  // The block's row offset goes in the per-lane offset, not the scalar
+  // offset: the buffer's range check covers only the per-lane offset (plus
+  // the immediate), so rows at or past Sk then read as zeros instead of
+  // whatever lies beyond the last key (the host keeps (Sk + 64) * ld * 2
+  // below 2^31, so the 32-bit sum cannot wrap).
   auto issue = [&](int j) {
     const int s = j % NS;
-    const int ko = j * KB * p.ldk * 2, vo = j * KB * p.ldv * 2;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rK, (lds_ptr_t)(&sK[s][0] + wave * 2048), 16, vk0, ko, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rK, (lds_ptr_t)(&sK[s][0] + wave * 2048 + 1024), 16, vk0 + k8, ko, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rV, (lds_ptr_t)(&sV[s][0] + wave * 2048), 16, vv0, vo, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rV, (lds_ptr_t)(&sV[s][0] + wave * 2048 + 1024), 16, vv0 + v8, vo, 0, 0);
+    const uint32_t ko = (uint32_t)j * (uint32_t)(KB * p.ldk * 2), vo = (uint32_t)j * (uint32_t)(KB * p.ldv * 2);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rK, (lds_ptr_t)(&sK[s][0] + wave * 2048), 16, vk0 + ko, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rK, (lds_ptr_t)(&sK[s][0] + wave * 2048 + 1024), 16, vk0 + k8 + ko, 0, 0,
+                                             0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rV, (lds_ptr_t)(&sV[s][0] + wave * 2048), 16, vv0 + vo, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rV, (lds_ptr_t)(&sV[s][0] + wave * 2048 + 1024), 16, vv0 + v8 + vo, 0, 0,
+                                             0);
   };
   issue(0);
   if (NB > 1) issue(1);

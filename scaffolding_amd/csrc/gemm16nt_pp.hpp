@@ -347,6 +347,11 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   if (grp == 0) __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
 
+  // The lane index is recomputed here rather than kept live across the
+  // main loop: with two M/N-contiguous operands the loop needs every
+  // register, and a value held across it would be spilled to scratch.
+  const int elane = lane_id_fresh();
+
   // ---- split tile: park the partial, the last part sums all of them ---------
   // Partials move with plain 16-byte stores and loads.  Each thread waits
   // for its own stores (vmcnt 0) before the workgroup barrier; the counter
@@ -354,7 +359,7 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   // (split_arrive), so the part that sees count split - 1 reads every other
   // part's data as written.
   if (NSTAGE == 2 && part >= 0) {
-    const int tid = threadIdx.x;
+    const int tid = wave * 64 + elane;
     float* mine = p.ws + (size_t)(split_tile * p.split + part) * (FN * FM * 512 * 4);
 #pragma unroll
     for (int i = 0; i < FN; ++i)
@@ -401,7 +406,7 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   for (int i = 0; i < FN; ++i) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) bv[i][q] = 0.f;
-    if (has_bias) load_bias4<TIn>(p.bias, n0 + wn * WN + i * 16 + 4 * (lane >> 4), N, bv[i]);
+    if (has_bias) load_bias4<TIn>(p.bias, n0 + wn * WN + i * 16 + 4 * (elane >> 4), N, bv[i]);
   }
   constexpr int PITCH = WN * 2 + 16;             // 144 bytes
   constexpr int ROWS_S = NSTAGE == 2 ? 64 : 32;  // 9216 / 4608 B per pass and wave
@@ -440,37 +445,37 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
 #pragma unroll
     for (int jj = 0; jj < ROWS_S / 16; ++jj) {
       const int j = ps * (ROWS_S / 16) + jj;
-      const int r = jj * 16 + (lane & 15);
+      const int r = jj * 16 + (elane & 15);
 #pragma unroll
       for (int i = 0; i < FN; ++i) {
         float v[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[q] = act_t<ACT>(acc[i][j][q] * alpha + bv[i][q]);
         if (R != nullptr) {
-          const int gm = m0 + wm * WM + j * 16 + (lane & 15);
+          const int gm = m0 + wm * WM + j * 16 + (elane & 15);
           if (gm < M) {
             float rr[4];
-            Res4<TOut>::load(R, (int64_t)gm * p.ldr, n0 + wn * WN + i * 16 + 4 * (lane >> 4), N, rvec, rr);
+            Res4<TOut>::load(R, (int64_t)gm * p.ldr, n0 + wn * WN + i * 16 + 4 * (elane >> 4), N, rvec, rr);
 #pragma unroll
             for (int q = 0; q < 4; ++q) v[q] += rr[q];
           }
         }
         const uint32_t lo = pack2<TOut>(v[0], v[1]);
         const uint32_t hi = pack2<TOut>(v[2], v[3]);
-        *reinterpret_cast<u32x2*>(stage + r * PITCH + (i * 16 + 4 * (lane >> 4)) * 2) = u32x2{lo, hi};
+        *reinterpret_cast<u32x2*>(stage + r * PITCH + (i * 16 + 4 * (elane >> 4)) * 2) = u32x2{lo, hi};
       }
     }
     wave_lds_sync();
     // All of this pass's staged row segments are read first (one LDS wait),
     // then stored.
     u32x4 vals[ROWS_S / ROWS_I];
-    const int cl = lane % LANES_ROW;
+    const int cl = elane % LANES_ROW;
 #pragma unroll
     for (int rr = 0; rr < ROWS_S / ROWS_I; ++rr)
-      vals[rr] = *reinterpret_cast<const u32x4*>(stage + (rr * ROWS_I + lane / LANES_ROW) * PITCH + cl * 16);
+      vals[rr] = *reinterpret_cast<const u32x4*>(stage + (rr * ROWS_I + elane / LANES_ROW) * PITCH + cl * 16);
 #pragma unroll
     for (int rr = 0; rr < ROWS_S / ROWS_I; ++rr) {
-      const int r = rr * ROWS_I + lane / LANES_ROW;
+      const int r = rr * ROWS_I + elane / LANES_ROW;
       const int gm = m0 + wm * WM + ps * ROWS_S + r;
       const int gn = n0 + wn * WN + cl * 8;
       const u32x4 val = vals[rr];

@@ -196,6 +196,15 @@ __device__ __forceinline__ void group_tile(int pid, int tiles_m, int tiles_n, in
   tn = r / gsize;
 }
 
+// The lane index (0..63) computed by v_mbcnt in volatile assembly, so the
+// compiler neither merges it with an earlier threadIdx.x nor keeps that
+// value alive across a loop: use it after register-heavy loops.
+__device__ __forceinline__ int lane_id_fresh() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 // Wave-wide sum / max through cross-lane permutes (64 lanes).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

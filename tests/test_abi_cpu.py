@@ -174,3 +174,24 @@ def test_bench_refuses_multi_gpu():
                        capture_output=True, text=True, timeout=300)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def test_split_tail_needs_whole_tiles_per_xcd():
+    """The tail split hands every XCD (tiles - tail) / 8 whole tiles, so it
+    is planned only when that divides evenly.  Run in a fresh process with
+    the host-only CU-count override (no device visible): M = 17776,
+    N = 1920, K = 7680 is 560 tiles; on 248 CUs 496 whole tiles remain
+    (divisible by 8: split), on 250 CUs 500 (not divisible: no split)."""
+    code = ("import ctypes,sys;so=ctypes.CDLL(sys.argv[1]);b=ctypes.create_string_buffer(96);I=ctypes.c_int64;"
+            "rc=so.sf_gemm_plan(0,1,I(17776),I(1920),I(7680),I(1),ctypes.c_void_p(256),I(7680),I(0),"
+            "ctypes.c_void_p(512),I(7680),I(0),ctypes.c_void_p(1024),I(1920),I(0),2,2,ctypes.c_float(1.0),"
+            "None,0,b,96);print(rc, b.value.decode())")
+    got = {}
+    for cus in (248, 250, 256):
+        env = dict(os.environ, SF_PLAN_CU_COUNT=str(cus), HIP_VISIBLE_DEVICES="-1")
+        r = subprocess.run([sys.executable, "-c", code, LIB], capture_output=True, text=True, timeout=120, env=env)
+        assert r.returncode == 0, r.stderr
+        got[cus] = r.stdout.strip()
+    assert got[256] == "0 gemm nt 256x256 lds-dma 16-bit split-tail 48x5"
+    assert got[248] == "0 gemm nt 256x256 lds-dma 16-bit split-tail 64x3"
+    assert got[250] == "0 gemm nt 256x256 lds-dma 16-bit"

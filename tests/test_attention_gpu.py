@@ -123,3 +123,38 @@ def test_abi_refusals():
     assert call(dt=0) == -3 and b"16-bit" in so.sf_last_error()
     assert call(ld=63) == -2
     cu().device_synchronize()
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("sk", [65, 100, 177, 4095])
+def test_rows_past_sk_are_never_read(dtype, sk):
+    """Keys and values past Sk inside the same allocation hold NaN: the
+    last, partial key block must read them as zeros (the buffer bound of
+    Sk rows), so the output stays finite and matches fp64.  Two batch
+    entries, each followed by 64 NaN rows, so entry 0's tail lies inside
+    entry 1's stride."""
+    b, sq, pad = 2, 130, 64
+    rng = np.random.default_rng(sk)
+    q = rnd(rng, (b, sq, 64), 1.0, dtype)
+    k = rnd(rng, (b, sk, 64), 1.0, dtype)
+    v = rnd(rng, (b, sk, 64), 1.0, dtype)
+    kp = np.full((b, sk + pad, 64), np.nan, np.float32)
+    vp = np.full((b, sk + pad, 64), np.nan, np.float32)
+    kp[:, :sk], vp[:, :sk] = k, v
+    g = cu()
+    gq, gk, gv = up(q, dtype), up(kp, dtype), up(vp, dtype)
+    go = up(np.zeros((b, sq, 64), np.float32), dtype)
+    so = ctypes.CDLL(os.path.join(ROOT, "scaffolding_amd", "libsfgemm.so"))
+    so.sf_last_error.restype = ctypes.c_char_p
+    I64, P = ctypes.c_int64, ctypes.c_void_p
+    st = (sk + pad) * 64
+    rc = so.sf_attention(P(gq.data_ptr), I64(64), I64(sq * 64), P(gk.data_ptr), I64(64), I64(st),
+                         P(gv.data_ptr), I64(64), I64(st), P(go.data_ptr), I64(64), I64(sq * 64),
+                         I64(b), I64(sq), I64(sk), I64(64), ctypes.c_float(0.125), 2 if dtype == "bfloat16" else 1,
+                         None)
+    assert rc == 0, so.sf_last_error()
+    g.device_synchronize()
+    o = down(go)
+    assert np.all(np.isfinite(o))
+    o64 = sdpa64(q, k, v, 0.125)
+    assert float(np.max(np.abs(o - o64))) <= bound(q, k, v, 0.125, dtype)
