@@ -136,6 +136,30 @@ int sf_gemm_add(int transA, int transB,
                 const void* bias, sf_epilogue epi,
                 const void* R, int64_t ldr, int64_t strideR, void* stream);
 
+/* sf_gemm for callers that cannot allocate device memory: code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc.  No
+ * counterpart in the reference (cuBLAS keeps its workspace internally).
+ *
+ * Same arguments, rules, kernels and results (bit for bit) as sf_gemm.  Where
+ * sf_gemm's plan splits tiles along k (it then allocates a per-device
+ * workspace on first use), this entry point takes the fp32 partials and the
+ * arrival counters from a fixed per-device scratch array of
+ * SF_NOALLOC_SCRATCH_BYTES inside the library, which each GPU the library
+ * runs on holds until the process ends; it calls no hipMalloc, hipFree or
+ * other allocating routine.  A plan whose workspace exceeds the scratch
+ * returns SF_ERR_UNSUPPORTED (no plan does on devices of up to 256 CUs).
+ * Every call on one device shares that device's scratch: calls that overlap
+ * on one device (different streams, or host threads without ordering) race;
+ * calls on one stream are ordered by it.  Asynchronous on `stream`. */
+#define SF_NOALLOC_SCRATCH_BYTES ((size_t)64 * 1024 * 1024 + 4096)
+int sf_gemm_noalloc(int transA, int transB,
+                    int64_t M, int64_t N, int64_t K, int64_t batch,
+                    const void* A, int64_t lda, int64_t strideA,
+                    const void* B, int64_t ldb, int64_t strideB,
+                    void* C, int64_t ldc, int64_t strideC,
+                    sf_dtype ab_dtype, sf_dtype c_dtype, float alpha,
+                    const void* bias, sf_epilogue epi, void* stream);
+
 /* Diagnostic twin of sf_gemm: validates the same arguments and writes the
  * name of the kernel sf_gemm would launch (e.g. "gemm tile 256x256",
  * "gemm skinny") into buf[len] without launching anything.  Host-only, no

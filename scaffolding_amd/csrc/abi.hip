@@ -282,22 +282,17 @@ const char* sf_last_error(void) { return g_err; }
 
 int sf_version(void) { return 100; /* 0.1.0 */ }
 
-// Validates sf_gemm's arguments and fills the launch plan.  Returns SF_OK
-// with *noop = true for an empty problem.  No HIP call before validation.
-struct GemmPlan {
-  GemmParams p;
-  int cfg;
-  bool fp32;
-  bool a_kmajor;
-  bool b_kmajor;
-  bool noop;
-};
+}  // extern "C"
 
-static int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t batch,
-                        const void* A, int64_t lda, int64_t strideA, const void* B, int64_t ldb,
-                        int64_t strideB, void* C, int64_t ldc, int64_t strideC, sf_dtype ab_dtype,
-                        sf_dtype c_dtype, float alpha, const void* bias, sf_epilogue epi,
-                        const void* R, int64_t ldr, int64_t strideR, bool need_c, GemmPlan& plan) {
+namespace sf {
+
+// Validates sf_gemm's arguments and fills the launch plan (GemmPlan,
+// sf_internal.hpp).  Returns SF_OK with plan.noop = true for an empty
+// problem.  No HIP call before validation.
+int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t batch, const void* A,
+                 int64_t lda, int64_t strideA, const void* B, int64_t ldb, int64_t strideB, void* C, int64_t ldc,
+                 int64_t strideC, sf_dtype ab_dtype, sf_dtype c_dtype, float alpha, const void* bias,
+                 sf_epilogue epi, const void* R, int64_t ldr, int64_t strideR, bool need_c, GemmPlan& plan) {
   g_err[0] = 0;
   plan.noop = false;
   if (!valid_dtype(ab_dtype) || !valid_dtype(c_dtype))
@@ -463,6 +458,30 @@ static int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K,
   return SF_OK;
 }
 
+void gemm_split_needs(const GemmPlan& plan, size_t* part_bytes, int* counters) {
+  *part_bytes = 0;
+  *counters = 0;
+  if (plan.noop || plan.p.split <= 0) return;
+  if (plan.fp32) {
+    const int tiles = plan.p.tiles_m * plan.p.tiles_n;
+    *part_bytes = (size_t)tiles * plan.p.split * (size_t)(plan.cfg == TILE_128x128 ? 16 : 4) * 256u * 16u;
+    *counters = tiles;
+  } else {
+    const int nsplit = plan.p.tiles_m * plan.p.tiles_n - plan.p.full_tiles;
+    *part_bytes = (size_t)nsplit * plan.p.split * (256u * 256u * 4u);
+    *counters = nsplit;
+  }
+}
+
+int gemm_launch_plan(const GemmPlan& plan, int64_t batch, sf_dtype ab_dtype, sf_dtype c_dtype, hipStream_t st) {
+  if (plan.fp32) return launch_gemm32(plan.a_kmajor, plan.b_kmajor, plan.cfg, plan.p, batch, st);
+  return launch_gemm16(ab_dtype, c_dtype, plan.a_kmajor, plan.b_kmajor, plan.cfg, plan.p, batch, st);
+}
+
+}  // namespace sf
+
+extern "C" {
+
 static int gemm_run(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t batch, const void* A,
                     int64_t lda, int64_t strideA, const void* B, int64_t ldb, int64_t strideB, void* C,
                     int64_t ldc, int64_t strideC, sf_dtype ab_dtype, sf_dtype c_dtype, float alpha,
@@ -473,26 +492,15 @@ static int gemm_run(int transA, int transB, int64_t M, int64_t N, int64_t K, int
                         strideC, ab_dtype, c_dtype, alpha, bias, epi, R, ldr, strideR, true, plan);
   if (rc != SF_OK || plan.noop) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (plan.fp32 && plan.p.split > 0) {
-    const int tiles = plan.p.tiles_m * plan.p.tiles_n;
-    const size_t part_bytes = (size_t)(plan.cfg == TILE_128x128 ? 16 : 4) * 256u * 16u;
-    rc = split_workspace_acquire((size_t)tiles * plan.p.split * part_bytes, tiles, st, &plan.p.ws, &plan.p.counters);
-    if (rc != SF_OK) return rc;
-    rc = launch_gemm32(plan.a_kmajor, plan.b_kmajor, plan.cfg, plan.p, batch, st);
-    const int rc2 = split_workspace_release(st);
-    return rc != SF_OK ? rc : rc2;
-  }
-  if (plan.fp32) return launch_gemm32(plan.a_kmajor, plan.b_kmajor, plan.cfg, plan.p, batch, st);
-  if (plan.p.split > 0) {
-    const int nsplit = plan.p.tiles_m * plan.p.tiles_n - plan.p.full_tiles;
-    rc = split_workspace_acquire((size_t)nsplit * plan.p.split * (256u * 256u * 4u), nsplit, st, &plan.p.ws,
-                                 &plan.p.counters);
-    if (rc != SF_OK) return rc;
-    rc = launch_gemm16(ab_dtype, c_dtype, plan.a_kmajor, plan.b_kmajor, plan.cfg, plan.p, batch, st);
-    const int rc2 = split_workspace_release(st);
-    return rc != SF_OK ? rc : rc2;
-  }
-  return launch_gemm16(ab_dtype, c_dtype, plan.a_kmajor, plan.b_kmajor, plan.cfg, plan.p, batch, st);
+  size_t part_bytes = 0;
+  int counters = 0;
+  gemm_split_needs(plan, &part_bytes, &counters);
+  if (part_bytes == 0) return gemm_launch_plan(plan, batch, ab_dtype, c_dtype, st);
+  rc = split_workspace_acquire(part_bytes, counters, st, &plan.p.ws, &plan.p.counters);
+  if (rc != SF_OK) return rc;
+  rc = gemm_launch_plan(plan, batch, ab_dtype, c_dtype, st);
+  const int rc2 = split_workspace_release(st);
+  return rc != SF_OK ? rc : rc2;
 }
 
 int sf_gemm(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t batch, const void* A,

@@ -42,6 +42,28 @@ int launch_gemm32(bool a_kmajor, bool b_kmajor, int cfg, const GemmParams& p, in
 // Tile edge of a config (BM, BN).
 void tile_dims(int cfg, bool fp32, int& bm, int& bn);
 
+// A validated GEMM launch: the kernel config and its parameters (abi.hip).
+struct GemmPlan {
+  GemmParams p;
+  int cfg;
+  bool fp32;
+  bool a_kmajor;
+  bool b_kmajor;
+  bool noop;  // an empty problem: nothing to launch
+};
+// Validates sf_gemm's arguments (R: residual of sf_gemm_add or NULL;
+// need_c: C must be non-NULL) and fills `plan`; no HIP call.
+int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t batch, const void* A,
+                 int64_t lda, int64_t strideA, const void* B, int64_t ldb, int64_t strideB, void* C, int64_t ldc,
+                 int64_t strideC, sf_dtype ab_dtype, sf_dtype c_dtype, float alpha, const void* bias,
+                 sf_epilogue epi, const void* R, int64_t ldr, int64_t strideR, bool need_c, GemmPlan& plan);
+// The split plan's workspace: fp32 partials (*part_bytes, 0 without a
+// split) followed by *counters ints that must be zero at launch.
+void gemm_split_needs(const GemmPlan& plan, size_t* part_bytes, int* counters);
+// Launches a plan whose workspace pointers (plan.p.ws, plan.p.counters)
+// are set when it splits.
+int gemm_launch_plan(const GemmPlan& plan, int64_t batch, sf_dtype ab_dtype, sf_dtype c_dtype, hipStream_t st);
+
 // Operands of one fused attention call (element strides): pair (b, h)
 // reads Q + b sQ + h hQ (rows of ldq), likewise K, V, and writes O.
 struct AttnShape {

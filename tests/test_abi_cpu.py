@@ -195,3 +195,20 @@ def test_split_tail_needs_whole_tiles_per_xcd():
     assert got[256] == "0 gemm nt 256x256 lds-dma 16-bit split-tail 48x5"
     assert got[248] == "0 gemm nt 256x256 lds-dma 16-bit split-tail 64x3"
     assert got[250] == "0 gemm nt 256x256 lds-dma 16-bit"
+
+
+def test_noalloc_rejects_plans_beyond_its_scratch():
+    """sf_gemm_noalloc runs sf_gemm's plans from a fixed scratch array; a plan
+    whose workspace would not fit is refused with a clear error before any
+    HIP call.  No 256-CU plan is that large, so a fresh process plans for
+    1024 CUs (host-only override): TN 2816 x 2816 x 4096 then splits 121
+    tiles 8 ways, 242 MB of partials."""
+    code = ("import ctypes,sys;so=ctypes.CDLL(sys.argv[1]);so.sf_last_error.restype=ctypes.c_char_p;"
+            "I=ctypes.c_int64;P=ctypes.c_void_p;"
+            "rc=so.sf_gemm_noalloc(1,0,I(2816),I(2816),I(4096),I(1),P(256),I(2816),I(0),P(512),I(2816),I(0),"
+            "P(1024),I(2816),I(0),2,2,ctypes.c_float(1.0),None,0,None);print(rc, so.sf_last_error().decode())")
+    env = dict(os.environ, SF_PLAN_CU_COUNT="1024", HIP_VISIBLE_DEVICES="-1")
+    r = subprocess.run([sys.executable, "-c", code, LIB], capture_output=True, text=True, timeout=120, env=env)
+    assert r.returncode == 0, r.stderr
+    rc, msg = r.stdout.strip().split(" ", 1)
+    assert int(rc) == -3 and "scratch" in msg and "253755392" in msg, r.stdout
