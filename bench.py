@@ -202,28 +202,35 @@ def sweep(d: Dev, steps: int, warmup: int, only: str | None):
         del ws
 
     # C4: fp16 attention, 60 heads x 4096 x 64.
-    if want("C4"):
+    c4 = ["C4_fp16_qkT_scaled", "C4_fp16_softmax", "C4_fp16_pv", "C4_fp16_sdpa_3kernel", "C4_fp16_sdpa_fused"]
+    if any(want(n) for n in c4):
         bh, s, dd = 60, 4096, 64
         q = d.rand((bh, s, dd), 1.0, np.float16)
         kk = d.rand((bh, s, dd), 1.0, np.float16)
         v = d.rand((bh, s, dd), 1.0, np.float16)
         st = max(3, steps // 10)
-        ms = d.time_steps(lambda i: cu.dev_batched_matmul_nt(q, kk, 0.125), st, 2)
-        rec("C4_fp16_qkT_scaled", ms, 2.0 * bh * s * s * dd, bh * (2 * s * dd + s * s) * 2.0, "hbm", PEAK_BF16)
-        scores = cu.dev_batched_matmul_nt(q, kk, 0.125)
-        ms = d.time_steps(lambda i: cu.dev_softmax(scores, -1), st, 2)
-        rec("C4_fp16_softmax", ms, 0.0, bh * s * s * 2 * 2.0, "hbm", PEAK_BF16)
-        probs = cu.dev_softmax(scores, -1)
-        del scores
-        ms = d.time_steps(lambda i: cu.dev_batched_matmul(probs, v), st, 2)
-        rec("C4_fp16_pv", ms, 2.0 * bh * s * s * dd, bh * (s * s + 2 * s * dd) * 2.0, "hbm", PEAK_BF16)
-        del probs
-        ms = d.time_steps(lambda i: cu.dev_sdpa_unfused(q, kk, v, 0.125), st, 1)
-        rec("C4_fp16_sdpa_3kernel", ms, 4.0 * bh * s * s * dd, bh * (4 * s * dd + 4 * s * s) * 2.0, "hbm",
-            PEAK_BF16)
-        # One fused launch (sf_attention): compute-bound, 4 * S^2 * D flop per head.
-        ms = d.time_steps(lambda i: cu.dev_scaled_dot_product_attention(q, kk, v, 0.125), max(5, steps // 2), 2)
-        rec("C4_fp16_sdpa_fused", ms, 4.0 * bh * s * s * dd, bh * 4 * s * dd * 2.0, "mfma", PEAK_BF16)
+        if want("C4_fp16_qkT_scaled"):
+            ms = d.time_steps(lambda i: cu.dev_batched_matmul_nt(q, kk, 0.125), st, 2)
+            rec("C4_fp16_qkT_scaled", ms, 2.0 * bh * s * s * dd, bh * (2 * s * dd + s * s) * 2.0, "hbm", PEAK_BF16)
+        if want("C4_fp16_softmax") or want("C4_fp16_pv"):
+            scores = cu.dev_batched_matmul_nt(q, kk, 0.125)
+            if want("C4_fp16_softmax"):
+                ms = d.time_steps(lambda i: cu.dev_softmax(scores, -1), st, 2)
+                rec("C4_fp16_softmax", ms, 0.0, bh * s * s * 2 * 2.0, "hbm", PEAK_BF16)
+            probs = cu.dev_softmax(scores, -1)
+            del scores
+            if want("C4_fp16_pv"):
+                ms = d.time_steps(lambda i: cu.dev_batched_matmul(probs, v), st, 2)
+                rec("C4_fp16_pv", ms, 2.0 * bh * s * s * dd, bh * (s * s + 2 * s * dd) * 2.0, "hbm", PEAK_BF16)
+            del probs
+        if want("C4_fp16_sdpa_3kernel"):
+            ms = d.time_steps(lambda i: cu.dev_sdpa_unfused(q, kk, v, 0.125), st, 1)
+            rec("C4_fp16_sdpa_3kernel", ms, 4.0 * bh * s * s * dd, bh * (4 * s * dd + 4 * s * s) * 2.0, "hbm",
+                PEAK_BF16)
+        if want("C4_fp16_sdpa_fused"):
+            # One fused launch (sf_attention): compute-bound, 4 * S^2 * D flop per head.
+            ms = d.time_steps(lambda i: cu.dev_scaled_dot_product_attention(q, kk, v, 0.125), max(5, steps // 2), 2)
+            rec("C4_fp16_sdpa_fused", ms, 4.0 * bh * s * s * dd, bh * 4 * s * dd * 2.0, "mfma", PEAK_BF16)
 
     # C5: bf16 DiT projections, 17776 tokens.
     tokens = 13 * (60 * 90 // 4) + 226
@@ -413,6 +420,60 @@ def trace_summary(path: str, last: int) -> None:
         len(d), name[:110], sum(d) / len(d), min(d), max(d)))
 
 
+def pmc_summary(path: str, kernel: str | None, last: int) -> None:
+    """Markdown summary of a rocprofv3 --pmc counter-collection CSV: for the
+    dispatches whose kernel name contains `kernel` (default: the most
+    dispatched kernel), the mean of each counter over the last `last` of
+    them, and derived figures where their counters are present:
+      clock      GRBM_GUI_ACTIVE / 8 XCDs / dispatch duration (the GRBM
+                 count is the sum over the 8 XCDs of gfx950)
+      MFMA busy  SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x GRBM_GUI_ACTIVE / 8)
+      co-exec    SQ_VALU_MFMA_COEXEC_CYCLES / SQ_VALU_MFMA_BUSY_CYCLES
+      L2 hit     TCC_HIT / (TCC_HIT + TCC_MISS)
+      L1->L2 latency  TCP_TCC_READ_REQ_LATENCY / TCP_TCC_READ_REQ (cycles)"""
+    import csv
+    disp = {}
+    for r in csv.DictReader(open(path)):
+        d = disp.setdefault(int(r["Dispatch_Id"]), {"name": r["Kernel_Name"]})
+        d[r["Counter_Name"]] = float(r["Counter_Value"])
+        d["dur_us"] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    names = {}
+    for d in disp.values():
+        names[d["name"]] = names.get(d["name"], 0) + 1
+    if kernel is None:
+        pick = max(names, key=names.get)
+        sel = [disp[i] for i in sorted(disp) if disp[i]["name"] == pick]
+    else:
+        sel = [disp[i] for i in sorted(disp) if kernel in disp[i]["name"]]
+    if not sel:
+        print("no dispatch matches %r" % kernel)
+        return
+    sel = sel[-last:]
+    keys = sorted(k for k in sel[0] if k != "name")
+    mean = {k: sum(d[k] for d in sel) / len(sel) for k in keys}
+    print("kernel `%s`, mean over its last %d dispatches\n" % (sel[-1]["name"][:110], len(sel)))
+    print("| counter | mean per dispatch |\n|---|---|")
+    for k in keys:
+        print("| %s | %.6g |" % (k, mean[k]))
+    der = []
+    gui = mean.get("GRBM_GUI_ACTIVE")
+    if gui:
+        der.append(("clock (GHz)", gui / 8 / mean["dur_us"] / 1e3))
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in mean:
+            der.append(("MFMA busy (fraction of SIMD cycles)", mean["SQ_VALU_MFMA_BUSY_CYCLES"] / 1024 / (gui / 8)))
+    if mean.get("SQ_VALU_MFMA_BUSY_CYCLES") and "SQ_VALU_MFMA_COEXEC_CYCLES" in mean:
+        der.append(("VALU co-executing with MFMA (fraction of MFMA-busy)",
+                    mean["SQ_VALU_MFMA_COEXEC_CYCLES"] / mean["SQ_VALU_MFMA_BUSY_CYCLES"]))
+    if "TCC_HIT" in mean and "TCC_MISS" in mean:
+        der.append(("L2 hit rate", mean["TCC_HIT"] / max(1.0, mean["TCC_HIT"] + mean["TCC_MISS"])))
+    if mean.get("TCP_TCC_READ_REQ") and "TCP_TCC_READ_REQ_LATENCY" in mean:
+        der.append(("L1->L2 read latency (cycles)", mean["TCP_TCC_READ_REQ_LATENCY"] / mean["TCP_TCC_READ_REQ"]))
+    if der:
+        print("\n| derived | value |\n|---|---|")
+        for k, v in der:
+            print("| %s | %.4g |" % (k, v))
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -425,12 +486,19 @@ def main(argv=None):
                     help="first run one fp32 x*1.0 pass over 1 GiB (reads 1 GiB, writes 1 GiB): the "
                          "known-traffic kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--no-headline", action="store_true")
+    ap.add_argument("--pmc-summary", default=None, metavar="CSV",
+                    help="print a markdown summary of a rocprofv3 --pmc counter-collection CSV (the last --steps "
+                         "dispatches of the kernel named by --kernel, default the most dispatched) and exit")
+    ap.add_argument("--kernel", default=None, help="kernel-name substring for --pmc-summary")
     ap.add_argument("--trace-summary", default=None, metavar="CSV",
                     help="print a markdown summary of a rocprofv3 kernel-trace CSV (the last --steps "
                          "dispatches of the most launched kernel separately) and exit; no GPU use")
     args = ap.parse_args(argv)
     if args.trace_summary:
         trace_summary(args.trace_summary, args.steps)
+        return 0
+    if args.pmc_summary:
+        pmc_summary(args.pmc_summary, args.kernel, args.steps)
         return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

@@ -38,10 +38,15 @@ extern "C" {
 /* Types and status codes                                              */
 /* ------------------------------------------------------------------ */
 
+/* The two sentinels of each enum give it the value range of int, so any
+ * int a caller passes (ctypes, FFI) is a valid value of the type in C++ and
+ * reaches the library's validation, which rejects it (SF_ERR_INVALID_ARG). */
 typedef enum {
+    SF_DTYPE_INVALID = -1,
     SF_F32 = 0,   /* IEEE binary32                                  */
     SF_F16 = 1,   /* IEEE binary16                                  */
-    SF_BF16 = 2   /* bfloat16 (upper half of binary32), stored u16  */
+    SF_BF16 = 2,  /* bfloat16 (upper half of binary32), stored u16  */
+    SF_DTYPE_RANGE_ = 0x7fffffff
 } sf_dtype;
 
 /* Epilogue applied to v = alpha * (op(A) . op(B)) in fp32 registers before
@@ -59,7 +64,9 @@ typedef enum {
     SF_EPI_BIAS_SILU = 2,
     SF_EPI_BIAS_GELU_TANH = 3,
     SF_EPI_SILU = 4,
-    SF_EPI_GELU_TANH = 5
+    SF_EPI_GELU_TANH = 5,
+    SF_EPI_INVALID = -1,
+    SF_EPI_RANGE_ = 0x7fffffff
 } sf_epilogue;
 
 #define SF_OK 0

@@ -30,6 +30,9 @@ int fail(int code, const char* fmt, ...) {
 
 int check_hip(hipError_t e, const char* what) {
   if (e == hipSuccess) return SF_OK;
+  // The runtime also keeps the error as the thread's last error; it is
+  // reported here, so it must not resurface in the next launch check.
+  (void)hipGetLastError();
   if (e == hipErrorOutOfMemory) return fail(SF_ERR_OOM, "%s: %s", what, hipGetErrorString(e));
   if (e == hipErrorNoDevice || e == hipErrorInvalidDevice)
     return fail(SF_ERR_NO_DEVICE, "%s: %s", what, hipGetErrorString(e));

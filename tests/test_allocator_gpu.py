@@ -77,3 +77,27 @@ def test_contents_survive_eviction(small_pool):
     tmp = [_buf(g, 30) for _ in range(2)]
     del tmp
     np.testing.assert_array_equal(g.gputensor_to_numpy(keep), np.arange(1 << 20, dtype=np.float32))
+
+
+def test_allocation_failure_raises_and_leaves_the_library_usable():
+    """An allocation the device cannot satisfy (64 TiB) fails the reference's
+    way: the C ABI returns a negative code (SF_ERR_OOM) with the detail in
+    sf_last_error, and the seam raises RuntimeError("CUDA error: ...")
+    (reference _cuda_kernels.cuh:303-319, _cuda_ops.pyx:292-300).  The
+    failure is not sticky: the next allocation and GEMM succeed."""
+    import ctypes
+    import os
+
+    g = cu()
+    with pytest.raises(RuntimeError, match="CUDA error: .*hipMalloc"):
+        g.empty((1 << 44,), np.float32)
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                                   "scaffolding_amd", "libsfgemm.so"))
+    lib.sf_last_error.restype = ctypes.c_char_p
+    p = ctypes.c_void_p()
+    got = ctypes.c_size_t()
+    rc = lib.sf_cache_alloc(0, ctypes.c_size_t(1 << 46), ctypes.byref(p), ctypes.byref(got))
+    assert rc == -5 and p.value is None and b"out of memory" in lib.sf_last_error().lower()
+    a = g.gputensor_from_numpy(np.eye(64, dtype=np.float32), 0, np.float32)
+    y = g.gputensor_to_numpy(g.dev_matmul(a, a))
+    assert np.array_equal(y, np.eye(64, dtype=np.float32))
