@@ -52,6 +52,10 @@ const char* tile_name(int cfg) {
     case TILE_SKINNY: return "gemm skinny";
     case TILE_NT_BIG: return "gemm nt 256x256 lds-dma";
     case TILE_SKINNY_LINE: return "gemm skinny line";
+    case TILE32_SMALL1: return "gemm small 16x16";
+    case TILE32_SMALL2: return "gemm small 16x32";
+    case TILE32_DMA: return "gemm tile 64x64 lds-dma k-groups";
+    case TILE32_DMA_SPLIT: return "gemm tile 64x64 lds-dma";
   }
   return "gemm";
 }
@@ -65,6 +69,8 @@ void tile_dims(int cfg, bool fp32, int& bm, int& bn) {
     case TILE_256x64: bm = 256; bn = 64; return;
     case TILE_SKINNY: bm = 16; bn = 32; return;
     case TILE_SKINNY_LINE: bm = 16; bn = 64; return;
+    case TILE32_SMALL1: bm = 16; bn = 16; return;
+    case TILE32_SMALL2: bm = 16; bn = 32; return;
     default: bm = 64; bn = 64; return;
   }
   (void)fp32;
@@ -149,8 +155,22 @@ static int choose_tile16(int64_t M, int64_t N, int64_t K, int64_t batch, bool ve
   return TILE_64x64;
 }
 
-static int choose_tile32(int64_t M, int64_t N, int64_t batch, bool vec, int cus) {
+// Picks the fp32 tile config.  Outputs of at most CUs / 4 tiles of 64 x 64
+// with K <= 2048 take the small-block kernel (16 x 16 blocks while they
+// number at most half the CUs, else 16 x 32); K-contiguous A with K % 32 ==
+// 0 takes the LDS-DMA kernel (two k-groups when the slice count is even);
+// the rest the register-staged tiles.  Measured: 64 x 512 x 512 NT 4.4 us
+// small 16 x 16 against 9.4 us for 64 x 64 tiles in 4 k-parts; 512^3 NN
+// 7.9 us small 16 x 32 against 12.5 us k-groups; 768 x 768 x 1024 NN 21.9 us
+// k-groups against 28.6 us small and 35 us register-staged in 7 k-parts;
+// 1024^3 NN 23.7 us k-groups against 27.1 us one group and 34 us
+// register-staged; 4096^3 NN 85% of the fp32 MFMA peak against 77%.
+static int choose_tile32(int64_t M, int64_t N, int64_t K, int64_t batch, bool vec, bool a_kmajor, bool dma_ok,
+                         int cus) {
   if (!vec) return TILE_GENERIC;
+  if (a_kmajor && 4 * cdiv(M, 64) * cdiv(N, 64) * batch <= cus && K <= 2048)
+    return 2 * cdiv(M, 16) * cdiv(N, 16) * batch <= cus ? TILE32_SMALL1 : TILE32_SMALL2;
+  if (dma_ok) return (K / 32) % 2 == 0 ? TILE32_DMA : TILE32_DMA_SPLIT;
   if (cdiv(M, 128) * cdiv(N, 128) * batch >= cus) return TILE_128x128;
   return TILE_64x64;
 }
@@ -364,8 +384,11 @@ int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
     const bool vec = al16(A) && al16(B) && (lda % 4 == 0) && (ldb % 4 == 0) &&
                      (strideA % 4 == 0) && (strideB % 4 == 0) && (K % 4 == 0) &&
                      (a_kmajor || M % 4 == 0) && (b_kmajor || N % 4 == 0);
+    // The LDS-DMA kernel addresses each operand with 32-bit byte offsets.
+    const bool dma_ok = a_kmajor && K % 32 == 0 && M * lda * 4 < (int64_t(1) << 31) &&
+                        (b_kmajor ? N : K) * ldb * 4 < (int64_t(1) << 31);
     plan.fp32 = true;
-    plan.cfg = choose_tile32(M, N, batch, vec, cus);
+    plan.cfg = choose_tile32(M, N, K, batch, vec, a_kmajor, dma_ok, cus);
   } else {
     const bool vec = al16(A) && al16(B) && (lda % 8 == 0) && (ldb % 8 == 0) &&
                      (strideA % 8 == 0) && (strideB % 8 == 0) && (K % 8 == 0) &&
@@ -391,6 +414,22 @@ int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
   p.split = 0;
   p.ws = nullptr;
   p.counters = nullptr;
+  if (plan.fp32 && batch == 1 && K >= 128 && (plan.cfg == TILE32_DMA || plan.cfg == TILE32_DMA_SPLIT)) {
+    // LDS-DMA fp32 with at most CUs / 4 tiles of 64 x 64 (K > 2048, past the
+    // small-block kernel): split every tile along k, at most 8 parts of at
+    // least 4 slices (64 x 4096 x 4096 NT: 37.9 us in 4 parts against
+    // 52 us small 16 x 32 blocks and 72 us unsplit; 200 x 300 x 4096 NN:
+    // 21.5 us in 8 parts against 71.6 us unsplit).  With more tiles two
+    // k-groups beat two k-parts (768 x 768 x 1024 NN: 21.9 us against 27 us).
+    const int64_t t64 = cdiv(M, 64) * cdiv(N, 64), KT = K / 32;
+    int64_t sp = cus / (t64 > 0 ? t64 : 1);
+    if (sp > kMaxSplit32) sp = kMaxSplit32;
+    if (sp > KT / 4) sp = KT / 4;
+    if (4 * t64 <= cus && sp >= 2) {
+      plan.cfg = TILE32_DMA_SPLIT;
+      p.split = (int)sp;
+    }
+  }
   if (plan.fp32 && batch == 1 && K >= 128 && (plan.cfg == TILE_128x128 || plan.cfg == TILE_64x64)) {
     // fp32 with fewer 64 x 64 tiles than CUs: split every tile along k (each
     // part at least 4 slices of 32), on 128 x 128 tiles when that reaches
@@ -400,7 +439,7 @@ int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
     const int64_t KT = cdiv(K, 32);
     auto parts = [&](int64_t t) {
       int64_t sp = cus / (t > 0 ? t : 1);
-      if (sp > 8) sp = 8;
+      if (sp > kMaxSplit32) sp = kMaxSplit32;
       if (sp > KT / 4) sp = KT / 4;
       return sp < 1 ? (int64_t)1 : sp;
     };

@@ -41,6 +41,10 @@
 
 namespace sf {
 
+// Most k-parts of an fp32 split-K tile (the kernels keep every part's
+// partial-sum loads in flight at once).
+constexpr int kMaxSplit32 = 8;
+
 struct GemmParams {
   const void* A;
   const void* B;
@@ -58,6 +62,8 @@ struct GemmParams {
   // fp32 partial tiles go to `ws` (256 KB each) and are summed, in part
   // order, by the part that finishes last (`counters`: one per split tile,
   // zero between launches).  split == 0: no tail split.
+  // fp32 kernels: every tile split into `split` parts (at most kMaxSplit32),
+  // one workgroup each, summed the same way.
   int full_tiles, split;
   float* ws;
   int* counters;

@@ -1,5 +1,7 @@
 // gemm32.hip — fp32 GEMM instantiations and launcher.
 #include "gemm32.hpp"
+#include "gemm32dma.hpp"
+#include "gemm32small.hpp"
 #include "sf_internal.hpp"
 
 namespace sf {
@@ -17,6 +19,22 @@ static int launch32_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hi
     case TILE_GENERIC:
       hipLaunchKernelGGL((gemm32_kernel<64, 64, 2, 2, KM, false, AKM>), g, dim3(256), 0, st, p);
       break;
+    case TILE32_SMALL1:
+    case TILE32_SMALL2:
+    case TILE32_DMA:
+    case TILE32_DMA_SPLIT:
+      if constexpr (AKM) {
+        if (cfg == TILE32_SMALL1)
+          hipLaunchKernelGGL((gemm32small_kernel<1, KM, 4>), g, dim3(256), 0, st, p);
+        else if (cfg == TILE32_SMALL2)
+          hipLaunchKernelGGL((gemm32small_kernel<2, KM, 8>), g, dim3(512), 0, st, p);
+        else if (cfg == TILE32_DMA)
+          hipLaunchKernelGGL((gemm32dma_kernel<64, 64, KM, 2, 2>), g, dim3(512), 0, st, p);
+        else
+          hipLaunchKernelGGL((gemm32dma_kernel<64, 64, KM, 3, 1>), g, dim3(256), 0, st, p);
+        break;
+      }
+      return fail(SF_ERR_INVALID_ARG, "tile config %d needs a K-contiguous A", cfg);
     default:
       return fail(SF_ERR_INVALID_ARG, "tile config %d has no fp32 variant", cfg);
   }
@@ -24,6 +42,10 @@ static int launch32_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hi
 }
 
 int launch_gemm32(bool a_kmajor, bool b_kmajor, int cfg, const GemmParams& p, int64_t batch, hipStream_t st) {
+  if (p.split > kMaxSplit32 || (p.split > 0 && batch != 1) || (cfg == TILE32_DMA && p.split > 0) ||
+      (cfg == TILE32_DMA && (p.K / 32) % 2 != 0))
+    return fail(SF_ERR_INVALID_ARG, "fp32 plan: split %d / batch %lld / K %d do not fit tile config %d", p.split,
+                (long long)batch, p.K, cfg);
   const unsigned gx = static_cast<unsigned>(p.tiles_m) * static_cast<unsigned>(p.tiles_n) *
                      static_cast<unsigned>(p.split > 0 ? p.split : 1);
   // grid.y is limited to 65535: walk the batch in chunks.

@@ -30,6 +30,52 @@
 
 namespace sf {
 
+// Split-K hand-off of an fp32 tile held as NF fragments per thread (flat
+// f32x4 array, fragment f of thread tid parked at ((f * NT) + tid) * 4 of
+// the part's slab): park this part's fragments, count the arrival, and in
+// the last part to arrive sum every part's fragments, this one's included,
+// in part order (the same additions whichever part is last).  Returns false
+// in every other part, which then has nothing left to do.  At most
+// kMaxSplit32 parts: each thread keeps all parts' loads of four fragments
+// in flight at once, so the sum costs one round trip per four fragments.
+template <int NF, int NT>
+__device__ __forceinline__ bool split32_handoff(f32x4* acc, const GemmParams& p, int tile_id, int part, int tid) {
+  static_assert(NF % 4 == 0, "partials move four fragments at a time");
+  float* mine = p.ws + (size_t)(tile_id * p.split + part) * (NF * NT * 4);
+#pragma unroll
+  for (int f = 0; f < NF; ++f) *reinterpret_cast<f32x4*>(mine + (size_t)(f * NT + tid) * 4) = acc[f];
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  __shared__ int arrived;
+  if (tid == 0) arrived = split_arrive(&p.counters[tile_id], p.split);
+  __syncthreads();
+  if (arrived != p.split - 1) return false;  // workgroup-uniform
+  const float* all = p.ws + (size_t)tile_id * p.split * (NF * NT * 4);
+#pragma unroll
+  for (int c = 0; c < NF / 4; ++c) {
+    f32x4 v[kMaxSplit32][4];
+#pragma unroll
+    for (int q = 0; q < kMaxSplit32; ++q) {
+      if (q < p.split) {
+        const float* src = all + ((size_t)q * NF + 4 * c) * NT * 4 + (size_t)tid * 4;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[q][u] = *reinterpret_cast<const f32x4*>(src + (size_t)u * NT * 4);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[4 * c + u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < kMaxSplit32; ++q) {
+      if (q < p.split) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[4 * c + u] += v[q][u];
+      }
+    }
+  }
+  if (tid == 0) __hip_atomic_store(&p.counters[tile_id], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool B_KMAJOR, bool VEC, bool A_KMAJOR = true>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm32_kernel(GemmParams p) {
   constexpr int NT = WAVES_M * WAVES_N * 64;
@@ -202,42 +248,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm32_kernel(GemmParam
   // ---- split-K: park the partial, the last part sums all of them in part
   // order (the same protocol as the 16-bit LDS-DMA kernel's split tail:
   // plain stores, the counter bumped by split_arrive, plain loads).
-  if (part >= 0) {
-    constexpr int NF = FN * FM;
-    float* mine = p.ws + (size_t)(tile_id * p.split + part) * (NF * NT * 4);
-#pragma unroll
-    for (int i = 0; i < FN; ++i)
-#pragma unroll
-      for (int j = 0; j < FM; ++j)
-        *reinterpret_cast<f32x4*>(mine + (size_t)((i * FM + j) * NT + tid) * 4) = acc[i][j];
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    __shared__ int arrived;
-    if (tid == 0) arrived = split_arrive(&p.counters[tile_id], p.split);
-    __syncthreads();
-    if (arrived != p.split - 1) return;  // workgroup-uniform
-    const float* all = p.ws + (size_t)tile_id * p.split * (NF * NT * 4);
-    static_assert(NF % 4 == 0, "partials move four fragments at a time");
-#pragma unroll
-    for (int c = 0; c < NF / 4; ++c) {
-      f32x4 sum[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) sum[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-      // Every part, this one included, is read back from the workspace: one
-      // straight-line loop, the same additions whichever part is last.
-      for (int q = 0; q < p.split; ++q) {
-        const float* src = all + ((size_t)q * NF + 4 * c) * NT * 4 + (size_t)tid * 4;
-        f32x4 v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const f32x4*>(src + (size_t)u * NT * 4);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) sum[u] += v[u];
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) acc[(4 * c + u) / FM][(4 * c + u) % FM] = sum[u];
-    }
-    if (tid == 0) __hip_atomic_store(&p.counters[tile_id], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  if (part >= 0 && !split32_handoff<FN * FM, NT>(&acc[0][0], p, tile_id, part, tid)) return;
 
   float* C = static_cast<float*>(p.C) + b * p.sC;
   const bool has_bias = epi_has_bias(p.epi);

@@ -26,7 +26,12 @@ enum TileCfg {
   TILE_GENERIC = 5,  // 64x64, element-wise bounds-checked loads (any layout)
   TILE_SKINNY = 6,   // M <= 16 stream kernel
   TILE_NT_BIG = 7,   // 256x256 NT, 8-wave ping-pong, direct-to-LDS (gemm16nt_pp.hpp)
-  TILE_SKINNY_LINE = 8  // M <= 16, K in {2048, 4096, 8192}: row-segment stream (skinny16l)
+  TILE_SKINNY_LINE = 8,  // M <= 16, K in {2048, 4096, 8192}: row-segment stream (skinny16l)
+  // fp32 only:
+  TILE32_SMALL1 = 9,     // 16x16 blocks, 4 waves splitting k (gemm32small.hpp)
+  TILE32_SMALL2 = 10,    // 16x32 blocks, 8 waves splitting k
+  TILE32_DMA = 11,       // 64x64, direct-to-LDS ring, two 4-wave k-groups (gemm32dma.hpp)
+  TILE32_DMA_SPLIT = 12  // 64x64, direct-to-LDS ring, one k-group, split-K capable
 };
 const char* tile_name(int cfg);
 

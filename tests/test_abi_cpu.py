@@ -128,9 +128,26 @@ def test_dispatch_for_config_shapes():
                 stride_c=4096 * 4096, dtype="float16").startswith("gemm nt 256x256 lds-dma")
     assert plan(transB=0, M=4096, N=64, K=4096, batch=60, ldb=64, ldc=64, stride_a=4096 * 4096,
                 stride_b=4096 * 64, stride_c=4096 * 64, dtype="float16").startswith("gemm tile 256x64")
-    # C1 / C2 fp32
-    assert plan(M=64, N=512, K=512, lda=512, ldb=512, ldc=512, dtype="float32").startswith("gemm tile 64x64 fp32")
-    assert plan(transB=0, dtype="float32").startswith("gemm tile 128x128 fp32")
+    # C1 / C2 fp32: outputs of at most CUs / 4 tiles of 64 x 64 with
+    # K <= 2048 -> small-block kernel (16 x 16 blocks up to half the CUs,
+    # then 16 x 32); K-contiguous A, K % 32 == 0 -> LDS-DMA 64 x 64 with two
+    # k-groups (one k-group, split-K, for few tiles and K > 2048); otherwise
+    # the register-staged tiles
+    assert plan(M=64, N=512, K=512, lda=512, ldb=512, ldc=512, dtype="float32") == "gemm small 16x16 fp32"
+    assert plan(transB=0, M=512, N=512, K=512, lda=512, ldb=512, ldc=512, dtype="float32") \
+        == "gemm small 16x32 fp32"
+    assert plan(transB=0, M=1024, N=1024, K=1024, lda=1024, ldb=1024, ldc=1024, dtype="float32") \
+        == "gemm tile 64x64 lds-dma k-groups fp32"
+    assert plan(transB=0, dtype="float32") == "gemm tile 64x64 lds-dma k-groups fp32"
+    assert plan(M=64, dtype="float32") == "gemm tile 64x64 lds-dma fp32 split-tail 64x4"
+    assert plan(M=4096, K=4064, lda=4064, ldb=4064, dtype="float32") == "gemm tile 64x64 lds-dma fp32"
+    assert plan(K=4004, lda=4004, ldb=4004, dtype="float32").startswith("gemm tile 128x128 fp32")
+    assert plan(transB=0, M=768, N=768, K=1024, lda=1024, ldb=768, ldc=768, dtype="float32") \
+        == "gemm tile 64x64 lds-dma k-groups fp32"
+    assert plan(transB=0, M=200, N=300, K=4096, lda=4096, ldb=300, ldc=300, dtype="float32") \
+        == "gemm tile 64x64 lds-dma fp32 split-tail 20x8"
+    assert plan(M=1000, N=900, K=100, lda=100, ldb=100, ldc=900, dtype="float32") == "gemm tile 64x64 fp32"
+    assert plan(M=300, N=260, K=1000, lda=1000, ldb=1000, ldc=260, dtype="float32") == "gemm small 16x32 fp32"
     # backward GEMMs: dW = dY^T X (A stored K x M) takes the register-staged
     # tiles, never the LDS-DMA or skinny kernels; dX = dY W is NN
     assert plan(transA=1, transB=0, M=1920, N=7680, K=17776, lda=1920, ldb=7680, ldc=7680) \

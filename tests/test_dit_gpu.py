@@ -136,9 +136,14 @@ RES_CASES = [  # (dtype, m, n, k, kernel name prefix)
     ("bfloat16", 300, 520, 264, "gemm tile"),
     ("bfloat16", 4096, 4096, 128, "gemm nt 256x256 lds-dma"),
     ("bfloat16", 4352, 4096, 4096, "gemm nt 256x256 lds-dma"),  # split tail
-    ("float32", 70, 200, 136, "gemm tile"),
-    ("float32", 64, 64, 1024, "gemm tile"),                   # fp32 split-K
-    ("float32", 5, 33, 20, "gemm"),
+    ("float32", 70, 200, 136, "gemm small 16x16"),
+    ("float32", 64, 64, 1024, "gemm small 16x16"),
+    ("float32", 5, 33, 20, "gemm small 16x16"),
+    ("float32", 200, 300, 1000, "gemm small 16x32"),
+    ("float32", 600, 520, 256, "gemm tile 64x64 lds-dma k-groups"),
+    ("float32", 600, 520, 160, "gemm tile 64x64 lds-dma fp32"),           # odd slice count: one k-group
+    ("float32", 64, 1000, 4096, "gemm tile 64x64 lds-dma fp32 split"),    # fp32 split-K
+    ("float32", 70, 200, 4004, "gemm tile 64x64 fp32 split"),             # K % 32 != 0: register-staged
 ]
 
 

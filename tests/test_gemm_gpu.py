@@ -155,6 +155,16 @@ TILE_CASES = [
     ("float32", False, 2048, 2048, 136, 1, "gemm tile 128x128"),
     ("float32", False, 1000, 900, 100, 1, "gemm tile 64x64"),
     ("float32", True, 333, 270, 99, 1, "gemm tile generic"),
+    ("float32", True, 64, 512, 512, 1, "gemm small 16x16"),
+    ("float32", False, 50, 72, 300, 3, "gemm small 16x16"),
+    ("float32", True, 200, 300, 1000, 1, "gemm small 16x32"),
+    ("float32", False, 512, 512, 512, 1, "gemm small 16x32"),
+    ("float32", False, 500, 508, 64, 2, "gemm tile 64x64 lds-dma k-groups"),
+    ("float32", False, 1000, 900, 256, 1, "gemm tile 64x64 lds-dma k-groups"),
+    ("float32", True, 1000, 900, 256, 1, "gemm tile 64x64 lds-dma k-groups"),
+    ("float32", False, 2048, 2048, 2048, 1, "gemm tile 64x64 lds-dma k-groups"),
+    ("float32", True, 300, 200, 160, 4, "gemm tile 64x64 lds-dma fp32"),
+    ("float32", False, 300, 200, 160, 4, "gemm tile 64x64 lds-dma fp32"),
 ]
 
 
@@ -331,11 +341,14 @@ def test_shape_errors():
 
 FP32_SPLIT = [
     # (M, N, K, transB, expected plan)
-    (64, 512, 512, True, "gemm tile 64x64 fp32 split-tail 8x4"),
-    (768, 768, 1024, False, "gemm tile 128x128 fp32 split-tail 36x7"),
-    (1024, 1024, 1024, False, "gemm tile 64x64 fp32"),
+    (64, 4096, 4096, True, "gemm tile 64x64 lds-dma fp32 split-tail 64x4"),
+    (200, 300, 4096, False, "gemm tile 64x64 lds-dma fp32 split-tail 20x8"),
+    (100, 1000, 2560, True, "gemm tile 64x64 lds-dma fp32 split-tail 32x8"),
     (500, 700, 3000, False, "gemm tile 128x128 fp32 split-tail 24x8"),
-    (300, 260, 1000, True, "gemm tile 64x64 fp32 split-tail 25x8"),
+    (300, 260, 3000, True, "gemm tile 64x64 fp32 split-tail 25x8"),
+    # not split, checked the same way (run-to-run bit identity included)
+    (64, 512, 512, True, "gemm small 16x16 fp32"),
+    (768, 768, 1024, False, "gemm tile 64x64 lds-dma k-groups fp32"),
 ]
 
 

@@ -5,8 +5,9 @@ per SIMD: <= 256 VGPRs); a change that pushes one of them past it makes the
 compiler spill to scratch memory, which costs a global-memory round trip per
 spilled access.  This test compiles the hot translation units for gfx950
 with the compiler's resource-usage report and fails on any scratch use by
-the ping-pong GEMM (gemm16nt_pp), the row-segment skinny stream (skinny16l)
-and the fused attention (attn64)."""
+the ping-pong GEMM (gemm16nt_pp), the row-segment skinny stream (skinny16l),
+the fused attention (attn64) and the fp32 LDS-DMA and small-block GEMMs
+(gemm32dma, gemm32small)."""
 from __future__ import annotations
 
 import concurrent.futures as cf
@@ -20,8 +21,8 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "scaffolding_amd", "csrc")
-HOT = ["gemm16_bf16.hip", "gemm16_f16.hip", "attention.hip"]
-WATCH = re.compile(r"gemm16nt_pp_kernel|skinny16l_kernel|attn64_kernel")
+HOT = ["gemm16_bf16.hip", "gemm16_f16.hip", "attention.hip", "gemm32.hip"]
+WATCH = re.compile(r"gemm16nt_pp_kernel|skinny16l_kernel|attn64_kernel|gemm32dma_kernel|gemm32small_kernel")
 
 
 def _hipcc():
@@ -67,7 +68,8 @@ def test_hot_kernels_do_not_spill():
             reports = list(ex.map(lambda s: _report(s, d), HOT))
     seen = [k for r in reports for k in _kernels(r) if WATCH.search(k[0])]
     names = " ".join(k[0] for k in seen)
-    for want in ("gemm16nt_pp_kernel", "skinny16l_kernel", "attn64_kernel"):
+    for want in ("gemm16nt_pp_kernel", "skinny16l_kernel", "attn64_kernel", "gemm32dma_kernel",
+                 "gemm32small_kernel"):
         assert want in names, "no %s instantiation found in the report" % want
     spilled = [k for k in seen if k[2] > 0]
     assert not spilled, "kernels using scratch (name, VGPRs, bytes/lane): %s" % spilled
