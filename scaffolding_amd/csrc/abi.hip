@@ -81,6 +81,8 @@ int launch_gemm16(sf_dtype in, sf_dtype out, bool a_kmajor, bool b_kmajor, int c
   unsigned gx;
   if (cfg == TILE_SKINNY)
     gx = static_cast<unsigned>((p.N + 31) / 32);
+  else if (p.persist > 0)
+    gx = static_cast<unsigned>(p.persist);
   else if (p.split > 0)
     gx = static_cast<unsigned>(p.full_tiles) +
          static_cast<unsigned>(p.tiles_m * p.tiles_n - p.full_tiles) * static_cast<unsigned>(p.split);
@@ -414,6 +416,7 @@ int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
   p.split = 0;
   p.ws = nullptr;
   p.counters = nullptr;
+  p.persist = 0;
   if (plan.fp32 && batch == 1 && K >= 128 && (plan.cfg == TILE32_DMA || plan.cfg == TILE32_DMA_SPLIT)) {
     // LDS-DMA fp32 with at most CUs / 4 tiles of 64 x 64 (K > 2048, past the
     // small-block kernel): split every tile along k, at most 8 parts of at
@@ -467,27 +470,42 @@ int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
   }
   if (plan.cfg == TILE_NT_BIG && batch == 1 && K >= 128) {
     // Tail split: with R = tiles % CUs left over after whole waves, run the
-    // last R tiles as R * s workgroups of K / s each (s <= CUs / R), so the
-    // last wave is full instead of R / CUs full.  With fewer tiles than
-    // half the CUs every tile is split (split-K).  Behind whole waves the
-    // tail is split only for tiles of at least 32 k-units (K >= 4096): the
-    // parts' L2 write-back and partial sums cost more than a short tail
-    // (M = 17776, N = 1920: K = 1920 runs 134 us unsplit against 148 us in
-    // 5 parts; K = 7680 runs 467 us in 5 parts against 560 us unsplit).
-    // The kernel gives every XCD (T - R) / 8 whole tiles, so the split is
-    // taken only when the whole tiles divide evenly over the XCDs (always
-    // true while the CU count is a multiple of 8).
+    // last R tiles as R * s parts of K / s each (s <= CUs / R), so the last
+    // wave is full instead of R / CUs full.  With fewer tiles than half the
+    // CUs every tile is split (split-K).  Behind whole waves the tail is
+    // split only for tiles of at least 32 k-units (K >= 4096): the parts'
+    // partial sums cost more than a short tail (M = 17776, N = 1920: K =
+    // 1920 runs 127 us unsplit against 130 us in 5 parts; K = 7680 runs
+    // 453 us in 5 parts against 535 us unsplit, both persistent).
+    //
+    // Persistent tiles (K-contiguous operands, more tiles than CUs, CU
+    // count a multiple of 8): one workgroup per CU walks its tiles, the
+    // next tile's first loads under the current tile's end.  Taken when the
+    // last round is at most half full or the tail is split; with a fuller
+    // last round the hardware's dynamic dispatch balances better (C5 QKV
+    // 1610 tiles 311 -> 301 us, MLP-up 2100 tiles 400 -> 387 us; C3 M = 4096
+    // 688 tiles 261 us one workgroup per tile against 270 us persistent).
+    // Its split tail packs each tile's parts onto one XCD, at most CUs / 8
+    // parts per XCD.
     const int64_t T = (int64_t)p.tiles_m * p.tiles_n, R = T % cus, units = (K + 127) / 128;
+    const bool can_persist = a_kmajor && b_kmajor && T > cus && cus % kNumXcd == 0;
     const int64_t min_units = T > R ? 32 : 2;
     if (R > 0 && 2 * R <= cus && units >= min_units && (T - R) % kNumXcd == 0) {
       int64_t sp = cus / R;
       if (sp > units) sp = units;
       if (sp > 8) sp = 8;
+      if (can_persist) {
+        const int64_t per_xcd = (R + kNumXcd - 1) / kNumXcd;  // tail tiles on the busiest XCD
+        const int64_t cap = (cus / kNumXcd) / per_xcd;
+        if (sp > cap) sp = cap;
+      }
       if (sp >= 2) {
         p.full_tiles = (int)(T - R);
         p.split = (int)sp;
+        if (can_persist) p.persist = cus;
       }
     }
+    if (p.split == 0 && can_persist && 2 * R <= cus) p.persist = cus;
   }
   if (plan.cfg == TILE_SKINNY_LINE) {
     // One workgroup per CU where N allows, at most 64 rows of W each.
@@ -577,10 +595,12 @@ int sf_gemm_plan(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
   int rc = gemm_prepare(transA, transB, M, N, K, batch, A, lda, strideA, B, ldb, strideB, C, ldc,
                         strideC, ab_dtype, c_dtype, alpha, bias, epi, nullptr, 0, 0, false, plan);
   if (rc != SF_OK) return rc;
-  char extra[48] = "";
+  char extra[64] = "";
   if (!plan.noop && plan.p.split > 0)
-    snprintf(extra, sizeof(extra), " split-tail %dx%d", plan.p.tiles_m * plan.p.tiles_n - plan.p.full_tiles,
-             plan.p.split);
+    snprintf(extra, sizeof(extra), "%s split-tail %dx%d", plan.p.persist > 0 ? " persistent" : "",
+             plan.p.tiles_m * plan.p.tiles_n - plan.p.full_tiles, plan.p.split);
+  else if (!plan.noop && plan.p.persist > 0)
+    snprintf(extra, sizeof(extra), " persistent");
   const char* name = plan.noop ? "noop" : tile_name(plan.cfg);
   if (!plan.noop && plan.cfg == TILE_NT_BIG)  // the LDS-DMA kernel takes every operand layout
     name = plan.a_kmajor ? (plan.b_kmajor ? "gemm nt 256x256 lds-dma" : "gemm nn 256x256 lds-dma")

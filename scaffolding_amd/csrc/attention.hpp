@@ -273,6 +273,11 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
     };
     expo(std::integral_constant<int, 0>{});
     __builtin_amdgcn_sched_barrier(0);
+    // Raised wave priority for the P V stretch, so a SIMD's arbiter favours
+    // the wave that is issuing MFMAs over its sibling (the other workgroup
+    // on the CU).  Measured A/B in one run, bit-identical output: C4 277 ->
+    // 262 us; no change on the 17776-key DiT shape.
+    __builtin_amdgcn_s_setprio(1);
     static_for<3>([&](auto i_c) {
       constexpr int I = decltype(i_c)::value;
       pv(std::integral_constant<int, I>{});
@@ -286,6 +291,7 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
       __builtin_amdgcn_sched_barrier(0);
     });
     pv(std::integral_constant<int, 3>{});
+    __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_sched_barrier(0);
   }
 

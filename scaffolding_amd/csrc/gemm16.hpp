@@ -72,6 +72,10 @@ struct GemmParams {
   // (same pointer and ldc): every element is read before it is written.
   const void* res;
   int64_t ldr, sR;
+  // 256 x 256 NT kernel, batch 1: > 0 runs the persistent variant on this
+  // many workgroups (one per CU, a multiple of 8); 0: one workgroup per
+  // tile (or split part).
+  int persist;
 };
 
 // Split-tile arrival, called by one thread of a workgroup after every
@@ -99,6 +103,27 @@ __device__ __forceinline__ int split_arrive(int* counter, int parts) {
   const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (before == parts - 1) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   return before;
+}
+
+// Split-tile arrival for parts that the launch places on one XCD (so they
+// share its L2): called by one thread after every thread's partial stores
+// completed (s_waitcnt vmcnt(0), workgroup barrier).  The stores are then
+// in the XCD's L2, where the last part reads them, so no L2 write-back or
+// invalidate is needed.  Each part checks that it really runs on the XCD
+// the launch intended (hardware register XCC_ID against `xcd`); one that
+// does not releases at agent scope (L2 write-back) and flags its arrival
+// (bit 16 and up), and the last part then acquires at agent scope before
+// reading.  Returns how many parts arrived before this one.
+__device__ __forceinline__ int split_arrive_xcd(int* counter, int parts, int xcd) {
+  const int xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20) & 15;  // HW_REG_XCC_ID[3:0]
+  const bool off = xcc != xcd;
+  if (off) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __builtin_amdgcn_s_waitcnt(0);
+  }
+  const int before = __hip_atomic_fetch_add(counter, off ? 0x10001 : 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if ((before & 0xffff) == parts - 1 && ((before >> 16) != 0 || off)) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  return before & 0xffff;
 }
 
 template <typename T> struct Mfma16;

@@ -56,6 +56,12 @@ static int launch16_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hi
           hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut, 1>), g, dim3(512), 0, st, p);
           break;
         }
+        if (p.persist > 0) {
+          if (p.K % 128 != 0 || p.persist % kNumXcd != 0 || gy != 1)
+            return fail(SF_ERR_INVALID_ARG, "persistent 256x256 kernel: K %% 128, grid %% 8 and batch 1 required");
+          hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut, 2, true, true, true>), g, dim3(512), 0, st, p);
+          break;
+        }
       }
       if (p.K % 128 != 0 && (AKM || KM))
         return fail(SF_ERR_INVALID_ARG, "the 256x256 LDS-DMA kernel needs K %% 128 == 0 with a K-contiguous operand");

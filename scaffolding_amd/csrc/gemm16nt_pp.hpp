@@ -59,6 +59,20 @@
 // Epilogue: alpha, bias and activation in registers, each wave stages its
 // 128 x 64 result through its own 16 KB of the stage arrays (64-row passes,
 // 144-byte pitch) and stores 128-byte row segments with 16-byte lanes.
+//
+// Persistent tiles (PERSIST, K-contiguous operands, batch 1): one
+// workgroup per CU walks a list of jobs — whole tiles in rounds of
+// gridDim.x, then at most one part of a split tail tile.  The k-pair stream
+// runs on across jobs: in the last pair of a job, the even step loads the
+// next job's first pair into the stage that pair KP - 2 has left (the same
+// rule as inside a job), so that load's latency hides under the job's last
+// two slices and its epilogue.  The epilogue stages through stage 1 only
+// (32-row passes) while stage 0 receives the next job's first pair; a
+// workgroup barrier after it frees stage 1 for the next job's second pair.
+// The split tail places every part of a tile on one XCD (tail tile t on XCD
+// t % 8, parts on consecutive workgroups of that XCD), so the partial-sum
+// hand-off goes through that XCD's L2 without write-back or invalidate
+// (split_arrive_xcd).
 #pragma once
 
 #include "gemm16.hpp"
@@ -116,9 +130,10 @@ constexpr int waitcnt_imm(int vm, int lgkm) {
 // exactly (one slice pair, e.g. attention scores Q.K^T at head size 64): a
 // single 64 KB stage, so two workgroups share a CU and one's stores overlap
 // the other's loads.
-template <typename TIn, typename TOut, int NSTAGE = 2, bool A_KM = true, bool B_KM = true>
+template <typename TIn, typename TOut, int NSTAGE = 2, bool A_KM = true, bool B_KM = true, bool PERSIST = false>
 __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   static_assert(NSTAGE == 1 || NSTAGE == 2, "one or two pair stages");
+  static_assert(!PERSIST || (NSTAGE == 2 && A_KM && B_KM), "persistent tiles: pipelined NT kernel only");
   static_assert(NSTAGE == 2 || (A_KM && B_KM), "K == 64 stage: K-contiguous operands only");
   constexpr int BM = 256, BN = 256, BK = 32;
   constexpr int WM = 128, WN = 64, FM = WM / 16, FN = WN / 16;
@@ -134,51 +149,89 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   const int wn = wave & 3;
 
   const int M = p.M, N = p.N, K = p.K;
-  int tm, tn;
-  // This workgroup's k slices [t_begin, t_begin + KT) and, in a split tile,
-  // its part index (-1: whole tile).
   // With two M/N-contiguous operands K need not be a multiple of 128: the
   // loop runs to the next multiple and the k-rows past K read as zeros
   // through both buffers' bounds.
   const int KU = (K + 4 * BK - 1) / (4 * BK);  // 128-k units
-  int t_begin = 0, KT = NSTAGE == 2 ? 4 * KU : K / BK, part = -1, split_tile = 0;
-  {
-    int pid;
-    int spid = -1;  // split part id
-    if (NSTAGE == 2 && p.split > 0) {
-      // Every XCD gets the same share of whole tiles (a contiguous range, as
-      // xcd_remap gives) followed by its share of split parts, so the XCDs
-      // finish together; within an XCD the long jobs are dispatched first.
-      const int xcd = blockIdx.x % kNumXcd, o = blockIdx.x / kNumXcd;
-      const int fx = p.full_tiles / kNumXcd;  // full_tiles is a multiple of the CU count
-      const int P = (p.tiles_m * p.tiles_n - p.full_tiles) * p.split;
-      if (o < fx) {
-        pid = xcd * fx + o;
-      } else {
-        spid = xcd * (P / kNumXcd) + (xcd < P % kNumXcd ? xcd : P % kNumXcd) + (o - fx);
-        pid = p.full_tiles + spid / p.split;
-      }
-    } else {
-      pid = xcd_remap(blockIdx.x, gridDim.x);
-    }
-    if (spid >= 0) {
-      const int r = spid / p.split, q = spid % p.split;
-      const int units = KU;
-      const int u0 = q * units / p.split, u1 = (q + 1) * units / p.split;
-      t_begin = 4 * u0;
-      KT = 4 * (u1 - u0);
-      part = q;
-      split_tile = r;
-      pid = p.full_tiles + r;
-    }
+  // A job: one output tile (pid), its k slices [t_begin, t_begin + KT) and,
+  // in a split tile, its part index (-1: whole tile) and split tile index.
+  struct Job {
+    int m0, n0, t_begin, KT, part, split_tile;
+  };
+  const int xcd = blockIdx.x % kNumXcd, xo = blockIdx.x / kNumXcd;
+  auto make_job = [&](int pid, int q, int st, Job& jb) {
+    int tm, tn;
     group_tile(pid, p.tiles_m, p.tiles_n, 8, tm, tn);
-  }
-  const int m0 = tm * BM;
-  const int n0 = tn * BN;
+    jb.m0 = tm * BM;
+    jb.n0 = tn * BN;
+    jb.part = q;
+    jb.split_tile = st;
+    if (q >= 0) {
+      const int u0 = q * KU / p.split, u1 = (q + 1) * KU / p.split;
+      jb.t_begin = 4 * u0;
+      jb.KT = 4 * (u1 - u0);
+    } else {
+      jb.t_begin = 0;
+      jb.KT = NSTAGE == 2 ? 4 * KU : K / BK;
+    }
+  };
+  // Job k of this workgroup; false when it has fewer jobs.
+  //  PERSIST: the grid is one workgroup per CU (a multiple of 8).  Round r
+  //   of the whole tiles is tile r * grid + slot (each XCD a contiguous
+  //   range of 32 tile ids per round).  With a split tail, the R leftover
+  //   tiles follow: tail tile t runs on XCD t % 8, as split parts on
+  //   consecutive workgroups of that XCD, so every part of a tile shares one
+  //   L2 (the partial-sum hand-off then needs no L2 write-back).
+  //  otherwise: one job per workgroup; split tails as before (whole tiles
+  //   first, then each XCD's share of the parts).
+  const int n_tiles = p.tiles_m * p.tiles_n;
+  auto job_at = [&](int k, Job& jb) -> bool {
+    if constexpr (PERSIST) {
+      const int G = (int)gridDim.x;
+      const int slot = xcd * (G / kNumXcd) + xo;
+      const int whole = p.split > 0 ? p.full_tiles : n_tiles;
+      const int nr = (whole + G - 1) / G;
+      if (k < nr) {
+        const int pid = k * G + slot;
+        if (pid >= whole) return false;
+        make_job(pid, -1, 0, jb);
+        return true;
+      }
+      if (p.split <= 0 || k > nr) return false;
+      const int t = (xo / p.split) * kNumXcd + xcd;
+      if (t >= n_tiles - p.full_tiles) return false;
+      make_job(p.full_tiles + t, xo % p.split, t, jb);
+      return true;
+    } else {
+      if (k > 0) return false;
+      if (NSTAGE == 2 && p.split > 0) {
+        // Every XCD gets the same share of whole tiles (a contiguous range,
+        // as xcd_remap gives) followed by its share of split parts, so the
+        // XCDs finish together; within an XCD the long jobs come first.
+        const int fx = p.full_tiles / kNumXcd;  // full_tiles is a multiple of the CU count
+        const int P = (n_tiles - p.full_tiles) * p.split;
+        if (xo < fx) {
+          make_job(xcd * fx + xo, -1, 0, jb);
+        } else {
+          const int spid = xcd * (P / kNumXcd) + (xcd < P % kNumXcd ? xcd : P % kNumXcd) + (xo - fx);
+          make_job(p.full_tiles + spid / p.split, spid % p.split, spid / p.split, jb);
+        }
+      } else {
+        make_job(xcd_remap(blockIdx.x, gridDim.x), -1, 0, jb);
+      }
+      return true;
+    }
+  };
+  Job cur, nxt;
+  if (!job_at(0, cur)) return;  // workgroup-uniform: no work at all
+  int jk = 0;
+  bool has_next = job_at(1, nxt);
+  int m0 = cur.m0, n0 = cur.n0;
+  int t_begin = cur.t_begin, KT = cur.KT, part = cur.part, split_tile = cur.split_tile;
   const int64_t b = blockIdx.y;
   const uint16_t* __restrict__ A = static_cast<const uint16_t*>(p.A) + b * p.sA;
   const uint16_t* __restrict__ B = static_cast<const uint16_t*>(p.B) + b * p.sB;
-  const int KP = KT / 2;  // slice pairs (KT a multiple of 4)
+  int KP = KT / 2;  // slice pairs (KT a multiple of 4)
 
   // A pair stage holds 64 k-columns: line r (128 B) is row r's 64 k values,
   // logical 16-byte chunk h (k = 8h .. 8h+7) at slot h ^ (r & 7).  Slice 2s
@@ -226,11 +279,25 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   } else {
     vob[0] = ((uint32_t)mrow * (uint32_t)p.ldb + (uint32_t)(n0 + mch * 8)) * 2u;
   }
+  // The next job's row offsets (persistent kernel: K-contiguous operands).
+  // Only the persistent kernel re-points the offsets; the one-job kernels
+  // keep the straight-line set-up above (written through this lambda, the
+  // both-M/N-contiguous kernel spilled two offsets to scratch).
+  auto set_offsets = [&](int am0, int bn0) {
+    if constexpr (PERSIST) {
+#pragma unroll
+      for (int i = 0; i < DMA_I; ++i) {
+        const int ga = am0 + drow + i * 8, gb = bn0 + drow + i * 8;
+        voa[i] = (uint32_t)(ga < M ? ga : M - 1) * (uint32_t)p.lda * 2u + dchunk_b;
+        vob[i] = (uint32_t)(gb < N ? gb : N - 1) * (uint32_t)p.ldb * 2u + dchunk_b;
+      }
+    }
+  };
   // With an M/N-contiguous operand beside it, a K-contiguous operand keeps
   // only its first row offset live and adds the 8-row steps at issue time
   // (the empty asm hides the value's invariance from loop hoisting): the
   // kernel then fits in 256 VGPRs without spills.
-  constexpr bool LEAN = !(A_KM && B_KM);
+  constexpr bool LEAN = !(A_KM && B_KM) || PERSIST;
   auto dma_op = [&](auto km_c, const __amdgpu_buffer_rsrc_t& rs, uint8_t* st, uint32_t* vo, int so, uint32_t step8) {
     constexpr bool KMJ = decltype(km_c)::value;
     if constexpr (KMJ && LEAN) asm volatile("" : "+v"(vo[0]));
@@ -247,19 +314,15 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
                                                  vo[0] + (uint32_t)so, 0, I * 128, 0);
     });
   };
-  auto dma = [&](uint8_t* sA, uint8_t* sB, int k0) {
-    const int kk = t_begin * BK + k0;  // first k of the pair
+  auto dma_at = [&](uint8_t* sA, uint8_t* sB, int kk) {  // kk: first k of the pair
     dma_op(std::integral_constant<bool, A_KM>{}, rA, sA, voa, A_KM ? kk * 2 : kk * (int)p.lda * 2,
            (uint32_t)p.lda * 16u);
     dma_op(std::integral_constant<bool, B_KM>{}, rB, sB, vob, B_KM ? kk * 2 : kk * (int)p.ldb * 2,
            (uint32_t)p.ldb * 16u);
   };
+  auto dma = [&](uint8_t* sA, uint8_t* sB, int k0) { dma_at(sA, sB, t_begin * BK + k0); };
 
   f32x4 acc[FN][FM];
-#pragma unroll
-  for (int i = 0; i < FN; ++i)
-#pragma unroll
-    for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   u32x4 ya[FM], xb[FN];
 
   // Fragment byte offsets for slice half 0 of a K-contiguous operand: A
@@ -294,7 +357,8 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
     return u32x4{lo[0], lo[1], hi[0], hi[1]};
   };
 
-  auto step = [&](int t, const uint8_t* sA, const uint8_t* sB, uint8_t* nA, uint8_t* nB) {
+  auto step = [&](int t, const uint8_t* sA, const uint8_t* sB, uint8_t* nA, uint8_t* nB, auto nxt_c) {
+    constexpr bool NXT = decltype(nxt_c)::value;  // load the next tile's first pair
     const bool odd = t & 1;  // static after unrolling
     // memory phase
     __builtin_amdgcn_sched_barrier(0);
@@ -310,7 +374,14 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
     });
     // Even t: the other pair stage was last read in step t-1, which both
     // groups finished before this phase; fill it with pair t/2 + 1.
-    if (!odd && t / 2 + 1 < KP) dma(nA, nB, (t + 2) * BK);
+    if constexpr (NXT) {
+      // last pair of this tile: the next tile's first pair goes into the
+      // stage whose slices (pair KP - 2) every wave has finished reading
+      set_offsets(nxt.m0, nxt.n0);
+      dma_at(nA, nB, nxt.t_begin * BK);
+    } else {
+      if (!odd && t / 2 + 1 < KP) dma(nA, nB, (t + 2) * BK);
+    }
     // Before step t+1 may read: if t+1 starts a new pair, this wave's loads of
     // that pair (issued in step t-1, nothing later yet) have landed.
     if (grp == 1 && odd)
@@ -332,17 +403,36 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   dma(sA0, sB0, 0);
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
   __builtin_amdgcn_s_barrier();
+  for (;;) {
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   if (grp == 1) __builtin_amdgcn_s_barrier();
+  constexpr std::false_type no_c{};
   if constexpr (NSTAGE == 2) {
-    for (int t = 0; t < KT; t += 4) {
-      step(t + 0, sA0, sB0, sA1, sB1);
-      step(t + 1, sA0, sB0, sA1, sB1);
-      step(t + 2, sA1, sB1, sA0, sB0);
-      step(t + 3, sA1, sB1, sA0, sB0);
+    if (PERSIST && has_next) {
+      for (int t = 0; t < KT - 4; t += 4) {
+        step(t + 0, sA0, sB0, sA1, sB1, no_c);
+        step(t + 1, sA0, sB0, sA1, sB1, no_c);
+        step(t + 2, sA1, sB1, sA0, sB0, no_c);
+        step(t + 3, sA1, sB1, sA0, sB0, no_c);
+      }
+      step(KT - 4, sA0, sB0, sA1, sB1, no_c);
+      step(KT - 3, sA0, sB0, sA1, sB1, no_c);
+      step(KT - 2, sA1, sB1, sA0, sB0, std::true_type{});
+      step(KT - 1, sA1, sB1, sA0, sB0, no_c);
+    } else {
+      for (int t = 0; t < KT; t += 4) {
+        step(t + 0, sA0, sB0, sA1, sB1, no_c);
+        step(t + 1, sA0, sB0, sA1, sB1, no_c);
+        step(t + 2, sA1, sB1, sA0, sB0, no_c);
+        step(t + 3, sA1, sB1, sA0, sB0, no_c);
+      }
     }
   } else {
-    step(0, sA0, sB0, sA0, sB0);  // KP == 1: no further pair is loaded
-    step(1, sA0, sB0, sA0, sB0);
+    step(0, sA0, sB0, sA0, sB0, no_c);  // KP == 1: no further pair is loaded
+    step(1, sA0, sB0, sA0, sB0, no_c);
   }
   if (grp == 0) __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
@@ -369,7 +459,9 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     __shared__ int arrived;
-    if (tid == 0) arrived = split_arrive(&p.counters[split_tile], p.split);
+    if (tid == 0)
+      arrived = PERSIST ? split_arrive_xcd(&p.counters[split_tile], p.split, xcd)
+                        : split_arrive(&p.counters[split_tile], p.split);
     __syncthreads();
     if (arrived != p.split - 1) return;  // workgroup-uniform
     // Sum the parts in part order (the same bits whichever part is last),
@@ -409,9 +501,12 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
     if (has_bias) load_bias4<TIn>(p.bias, n0 + wn * WN + i * 16 + 4 * (elane >> 4), N, bv[i]);
   }
   constexpr int PITCH = WN * 2 + 16;             // 144 bytes
-  constexpr int ROWS_S = NSTAGE == 2 ? 64 : 32;  // 9216 / 4608 B per pass and wave
+  constexpr int ROWS_S = (NSTAGE == 2 && !PERSIST) ? 64 : 32;  // 9216 / 4608 B per pass and wave
   uint8_t* stage;
-  if constexpr (NSTAGE == 2) {
+  if constexpr (PERSIST) {
+    // stage 0 is receiving the next tile's first pair: stage 1 only
+    stage = ((wave >> 2) ? sB1 : sA1) + (wave & 3) * (ROWS_S * PITCH);
+  } else if constexpr (NSTAGE == 2) {
     switch (wave >> 1) {
       case 0: stage = sA0; break;
       case 1: stage = sB0; break;
@@ -492,6 +587,21 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
     }
   }
   });
+  if (!has_next) break;
+  // every wave is done with the staging area (stage 1) before the next
+  // tile's second pair is loaded into it; then group 1 drops half a step
+  __syncthreads();
+  cur = nxt;
+  ++jk;
+  has_next = job_at(jk + 1, nxt);
+  m0 = cur.m0;
+  n0 = cur.n0;
+  t_begin = cur.t_begin;
+  KT = cur.KT;
+  KP = KT / 2;
+  part = cur.part;
+  split_tile = cur.split_tile;
+  }
 }
 
 }  // namespace sf

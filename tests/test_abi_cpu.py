@@ -110,14 +110,30 @@ def test_dispatch_for_config_shapes():
     assert plan().startswith("gemm nt 256x256 lds-dma")
     assert plan(M=4096, N=11008, ldc=11008).startswith("gemm nt 256x256 lds-dma")
     assert plan(M=17776, N=1920, K=7680, lda=7680, ldb=7680, ldc=1920).startswith("gemm nt 256x256 lds-dma")
-    # C5 tails (560 / 1610 / 2100 tiles): behind whole waves only K >= 4096
+    # C5 tails (560 / 1610 / 2100 tiles): persistent tiles (more tiles than
+    # CUs, last round at most half full); behind whole waves only K >= 4096
     # splits the last wave (MLP-down); out-projection, QKV and MLP-up run it
     # unsplit
     assert plan(M=17776, N=1920, K=7680, lda=7680, ldb=7680, ldc=1920) \
-        == "gemm nt 256x256 lds-dma 16-bit split-tail 48x5"
-    assert plan(M=17776, N=1920, K=1920, lda=1920, ldb=1920, ldc=1920) == "gemm nt 256x256 lds-dma 16-bit"
-    assert plan(M=17776, N=5760, K=1920, lda=1920, ldb=1920, ldc=5760) == "gemm nt 256x256 lds-dma 16-bit"
-    assert plan(M=17776, N=7680, K=1920, lda=1920, ldb=1920, ldc=7680) == "gemm nt 256x256 lds-dma 16-bit"
+        == "gemm nt 256x256 lds-dma 16-bit persistent split-tail 48x5"
+    assert plan(M=17776, N=1920, K=1920, lda=1920, ldb=1920, ldc=1920) \
+        == "gemm nt 256x256 lds-dma 16-bit persistent"
+    assert plan(M=17776, N=5760, K=1920, lda=1920, ldb=1920, ldc=5760) \
+        == "gemm nt 256x256 lds-dma 16-bit persistent"
+    assert plan(M=17776, N=7680, K=1920, lda=1920, ldb=1920, ldc=7680) \
+        == "gemm nt 256x256 lds-dma 16-bit persistent"
+    # one tile per CU (north star) and a last round more than half full
+    # (C3 M = 4096: 688 tiles) keep one workgroup per tile
+    assert plan() == "gemm nt 256x256 lds-dma 16-bit"
+    assert plan(M=4096, N=11008, ldc=11008) == "gemm nt 256x256 lds-dma 16-bit"
+    # whole rounds only: persistent; a split tail packs each XCD with at most
+    # 32 parts (85 tail tiles: 11 on the busiest XCD, so 2 parts each)
+    assert plan(N=8192, K=512, lda=512, ldb=512, ldc=8192) == "gemm nt 256x256 lds-dma 16-bit persistent"
+    assert plan(M=7900, N=2800, K=4352, lda=4352, ldb=4352, ldc=2800) \
+        == "gemm nt 256x256 lds-dma 16-bit persistent split-tail 85x2"
+    # backward layouts keep one workgroup per tile or split part
+    assert plan(transA=1, transB=0, M=4352, N=4096, K=4096, lda=4352, ldb=4096) \
+        == "gemm tn 256x256 lds-dma 16-bit split-tail 16x8"
     # C3 decode shapes -> row-segment stream kernel (K = 512 x waves)
     assert plan(M=1, N=11008, ldc=11008).startswith("gemm skinny line")
     assert plan(M=16, N=11008, ldc=11008).startswith("gemm skinny line")
@@ -195,10 +211,12 @@ def test_bench_refuses_multi_gpu():
 
 def test_split_tail_needs_whole_tiles_per_xcd():
     """The tail split hands every XCD (tiles - tail) / 8 whole tiles, so it
-    is planned only when that divides evenly.  Run in a fresh process with
-    the host-only CU-count override (no device visible): M = 17776,
-    N = 1920, K = 7680 is 560 tiles; on 248 CUs 496 whole tiles remain
-    (divisible by 8: split), on 250 CUs 500 (not divisible: no split)."""
+    is planned only when that divides evenly; the persistent kernel needs a
+    CU count that is a multiple of 8.  Run in a fresh process with the
+    host-only CU-count override (no device visible): M = 17776, N = 1920,
+    K = 7680 is 560 tiles; on 248 CUs 496 whole tiles remain (persistent,
+    split: at most 31 parts per XCD, 8 tail tiles on each, so 3 parts), on
+    250 CUs 500 (neither persistent nor split)."""
     code = ("import ctypes,sys;so=ctypes.CDLL(sys.argv[1]);b=ctypes.create_string_buffer(96);I=ctypes.c_int64;"
             "rc=so.sf_gemm_plan(0,1,I(17776),I(1920),I(7680),I(1),ctypes.c_void_p(256),I(7680),I(0),"
             "ctypes.c_void_p(512),I(7680),I(0),ctypes.c_void_p(1024),I(1920),I(0),2,2,ctypes.c_float(1.0),"
@@ -209,8 +227,8 @@ def test_split_tail_needs_whole_tiles_per_xcd():
         r = subprocess.run([sys.executable, "-c", code, LIB], capture_output=True, text=True, timeout=120, env=env)
         assert r.returncode == 0, r.stderr
         got[cus] = r.stdout.strip()
-    assert got[256] == "0 gemm nt 256x256 lds-dma 16-bit split-tail 48x5"
-    assert got[248] == "0 gemm nt 256x256 lds-dma 16-bit split-tail 64x3"
+    assert got[256] == "0 gemm nt 256x256 lds-dma 16-bit persistent split-tail 48x5"
+    assert got[248] == "0 gemm nt 256x256 lds-dma 16-bit persistent split-tail 64x3"
     assert got[250] == "0 gemm nt 256x256 lds-dma 16-bit"
 
 

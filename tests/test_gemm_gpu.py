@@ -273,15 +273,20 @@ def test_skinny_line_fp32_output():
 SPLIT_CASES = [
     # (M, N, K, act, bias, expected "split-tail R x s")
     (4352, 4096, 4096, None, False, "split-tail 16x8"),    # 272 tiles: 16 left over, 8 parts of 4 units
-    (7900, 2800, 4352, "gelu", True, "split-tail 85x3"),  # 341 tiles: 85 left, 34 units in 3 uneven parts
+    (7900, 2800, 4352, "gelu", True, "split-tail 85x2"),  # 341 tiles: 85 left, 34 units in 2 parts (XCD packing)
     (17776, 1920, 7680, None, True, "split-tail 48x5"),   # C5 MLP-down shape
+    # persistent tiles without a split: 2 rounds + 15 tiles; two whole rounds
+    (4352, 7936, 1024, "silu", True, "persistent"),
+    (4096, 8192, 512, None, True, "persistent"),
 ]
 
 
 @pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: "%dx%dx%d" % c[:3])
 def test_split_tail_linear(case):
     """The 256x256 NT kernel with its last partial wave of tiles split over k:
-    fp32 partials in a workspace, summed in part order by the last part.
+    fp32 partials in a workspace, summed in part order by the last part
+    (persistent tiles: the parts of a tile on one XCD); and persistent tiles
+    without a split.
     Two launches in a row check that the per-tile counters reset; sampled
     rows (including every split tile's rows) against fp64, checksums over all."""
     m, n, k, act, bias, expect = case

@@ -48,7 +48,7 @@ def _call(lib, fn, ta, tb, m, n, k, a, lda, b, ldb, c, dt):
 # scratch, then a smaller TT split-K (8 MB), fp32 split-K (2 MB), and no
 # split (fp32 small blocks, 16-bit tiles).
 CASES = [
-    ("bfloat16", 0, 4352, 4096, 4096, "gemm nt 256x256 lds-dma 16-bit split-tail 16x8"),
+    ("bfloat16", 0, 4352, 4096, 4096, "gemm nt 256x256 lds-dma 16-bit persistent split-tail 16x8"),
     ("bfloat16", 1, 1024, 1024, 4096, "gemm tt 256x256 lds-dma 16-bit split-tail 16x8"),
     ("float32", 0, 64, 1000, 4096, "gemm tile 64x64 lds-dma fp32 split-tail 16x8"),
     ("float32", 0, 64, 512, 512, "gemm small 16x16 fp32"),
