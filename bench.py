@@ -301,6 +301,18 @@ def sweep(d: Dev, steps: int, warmup: int, only: str | None):
         ms = d.time_steps(lambda i: cu.dev_linear_forward(x, w, b, "silu"), steps, warmup)
         rec("north_star_bf16_linear_bias_silu_4096", ms, 2.0 * 4096 ** 3, 3 * 4096 * 4096 * 2.0, "mfma",
             PEAK_BF16)
+    # Power probe, not a config: the headline GEMM (same kernel, same plan)
+    # on constant operands (x = 1, W = 1/128, b = 0: every product and sum
+    # is exact), whose multiplier inputs never toggle.  The gap to the
+    # random-operand headline is what the chip's power limit takes.
+    if want("power_probe"):
+        m = n = k = 4096
+        x = cu.gputensor_from_numpy(np.ones((m, k), np.float32), 0, "bfloat16")
+        w = cu.gputensor_from_numpy(np.full((n, k), 1.0 / 128, np.float32), 0, "bfloat16")
+        b = cu.gputensor_from_numpy(np.zeros((n,), np.float32), 0, "bfloat16")
+        ms = d.time_steps(lambda i: cu.dev_linear_forward(x, w, b), steps, warmup)
+        rec("power_probe_north_star_constant_operands", ms, 2.0 * m * n * k,
+            float((m * k + n * k + m * n) * 2 + n * 2), "mfma", PEAK_BF16)
     return out
 
 
