@@ -301,6 +301,14 @@ def sweep(d: Dev, steps: int, warmup: int, only: str | None):
         ms = d.time_steps(lambda i: cu.dev_linear_forward(x, w, b, "silu"), steps, warmup)
         rec("north_star_bf16_linear_bias_silu_4096", ms, 2.0 * 4096 ** 3, 3 * 4096 * 4096 * 2.0, "mfma",
             PEAK_BF16)
+    # HBM write probe, not a config: the library's zero fill (16-byte stores,
+    # grid-stride) over 1 GiB, a write-only stream like the C4 score kernel's
+    # 2 GB of output (the timing loop keeps 8 outputs live: 8 GiB, within
+    # the caching allocator's limit, so no allocation in the timed region).
+    if want("hbm_write_probe"):
+        n1g = (1 << 30) // 4
+        ms = d.time_steps(lambda i: cu.zeros((n1g,), np.float32, 0), max(5, steps // 4), warmup)
+        rec("hbm_write_probe_zero_fill_1GiB", ms, 0.0, float(1 << 30), "hbm", PEAK_BF16)
     # Power probe, not a config: the headline GEMM (same kernel, same plan)
     # on constant operands (x = 1, W = 1/128, b = 0: every product and sum
     # is exact), whose multiplier inputs never toggle.  The gap to the

@@ -417,6 +417,7 @@ int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
   p.ws = nullptr;
   p.counters = nullptr;
   p.persist = 0;
+  p.xcd_shift = 0;
   if (plan.fp32 && batch == 1 && K >= 128 && (plan.cfg == TILE32_DMA || plan.cfg == TILE32_DMA_SPLIT)) {
     // LDS-DMA fp32 with at most CUs / 4 tiles of 64 x 64 (K > 2048, past the
     // small-block kernel): split every tile along k, at most 8 parts of at
@@ -502,7 +503,14 @@ int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
       if (sp >= 2) {
         p.full_tiles = (int)(T - R);
         p.split = (int)sp;
-        if (can_persist) p.persist = cus;
+        if (can_persist) {
+          p.persist = cus;
+          // Test hook: SF_TEST_XCD_SHIFT = s (1..7) makes every part expect
+          // the XCD s places away from its own, so each takes the agent-scope
+          // fallback hand-off; the results must not change.
+          const char* sh = getenv("SF_TEST_XCD_SHIFT");
+          p.xcd_shift = sh != nullptr ? (atoi(sh) & (kNumXcd - 1)) : 0;
+        }
       }
     }
     if (p.split == 0 && can_persist && 2 * R <= cus) p.persist = cus;

@@ -76,6 +76,10 @@ struct GemmParams {
   // many workgroups (one per CU, a multiple of 8); 0: one workgroup per
   // tile (or split part).
   int persist;
+  // Added to the XCD a persistent split part expects to run on (0 in
+  // production).  A test sets it to make every part see itself off its XCD
+  // and take the agent-scope fallback of split_arrive_xcd.
+  int xcd_shift;
 };
 
 // Split-tile arrival, called by one thread of a workgroup after every

@@ -460,7 +460,7 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
     __syncthreads();
     __shared__ int arrived;
     if (tid == 0)
-      arrived = PERSIST ? split_arrive_xcd(&p.counters[split_tile], p.split, xcd)
+      arrived = PERSIST ? split_arrive_xcd(&p.counters[split_tile], p.split, (xcd + p.xcd_shift) & (kNumXcd - 1))
                         : split_arrive(&p.counters[split_tile], p.split);
     __syncthreads();
     if (arrived != p.split - 1) return;  // workgroup-uniform

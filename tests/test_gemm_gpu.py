@@ -281,6 +281,36 @@ SPLIT_CASES = [
 ]
 
 
+def test_persistent_split_off_xcd_fallback():
+    """The persistent split tail places every part of a tile on one XCD and
+    hands partials over through that XCD's L2.  A part that finds itself on
+    another XCD (hardware XCC_ID) releases at agent scope and makes the last
+    part acquire.  SF_TEST_XCD_SHIFT makes every part expect a different XCD,
+    so all of them take that fallback: the output must be bit-identical to
+    the same-XCD hand-off (same parts, same summation order)."""
+    m, n, k = 4352, 4096, 4096
+    rng = np.random.default_rng(77)
+    x = rnd(rng, (m, k), 1.0, "bfloat16")
+    w = rnd(rng, (n, k), 1.0 / np.sqrt(k), "bfloat16")
+    gx, gw = up(x, "bfloat16"), up(w, "bfloat16")
+    plan = cu().gemm_plan(1, m, n, k, 1, gx.data_ptr, k, 0, gw.data_ptr, k, 0, n, 0, gx.dtype)
+    assert plan.endswith("persistent split-tail 16x8"), plan
+    y0 = down(cu().dev_linear_forward(gx, gw, None))
+    os.environ["SF_TEST_XCD_SHIFT"] = "3"
+    try:
+        y1 = down(cu().dev_linear_forward(gx, gw, None))
+        y2 = down(cu().dev_linear_forward(gx, gw, None))
+    finally:
+        del os.environ["SF_TEST_XCD_SHIFT"]
+    y3 = down(cu().dev_linear_forward(gx, gw, None))
+    for y in (y1, y2, y3):
+        assert np.array_equal(y.view(np.uint32), y0.view(np.uint32)), "fallback hand-off changed the output"
+    rows = np.r_[0, 1000, m - 256, m - 1]
+    y64 = ref.linear_f64(x[rows], w, None, None)
+    absprod = np.abs(x[rows].astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+    check_bound(y0[rows], y64, gemm_bound(y64, absprod, k, "bfloat16", None), "persistent split")
+
+
 @pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: "%dx%dx%d" % c[:3])
 def test_split_tail_linear(case):
     """The 256x256 NT kernel with its last partial wave of tiles split over k:
