@@ -418,6 +418,7 @@ int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
   p.counters = nullptr;
   p.persist = 0;
   p.xcd_shift = 0;
+  p.arrive_spins = kSplitArriveSpins;
   if (plan.fp32 && batch == 1 && K >= 128 && (plan.cfg == TILE32_DMA || plan.cfg == TILE32_DMA_SPLIT)) {
     // LDS-DMA fp32 with at most CUs / 4 tiles of 64 x 64 (K > 2048, past the
     // small-block kernel): split every tile along k, at most 8 parts of at
@@ -474,10 +475,11 @@ int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
     // last R tiles as R * s parts of K / s each (s <= CUs / R), so the last
     // wave is full instead of R / CUs full.  With fewer tiles than half the
     // CUs every tile is split (split-K).  Behind whole waves the tail is
-    // split only for tiles of at least 32 k-units (K >= 4096): the parts'
-    // partial sums cost more than a short tail (M = 17776, N = 1920: K =
-    // 1920 runs 127 us unsplit against 130 us in 5 parts; K = 7680 runs
-    // 453 us in 5 parts against 535 us unsplit, both persistent).
+    // split for tiles of at least 32 k-units (K >= 4096), and in short
+    // persistent launches (below) from 8 units: otherwise the parts' partial
+    // sums cost more than a short tail (M = 17776, N = 1920: K = 1920 with
+    // one part summing all: 127 us unsplit against 130 us in 5 parts; K =
+    // 7680 runs 453 us in 5 parts against 535 us unsplit, both persistent).
     //
     // Persistent tiles (K-contiguous operands, more tiles than CUs, CU
     // count a multiple of 8): one workgroup per CU walks its tiles, the
@@ -487,13 +489,22 @@ int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
     // 1610 tiles 311 -> 301 us, MLP-up 2100 tiles 400 -> 387 us; C3 M = 4096
     // 688 tiles 261 us one workgroup per tile against 270 us persistent).
     // Its split tail packs each tile's parts onto one XCD, at most CUs / 8
-    // parts per XCD.
+    // parts per XCD, and shares the final sum among the parts (each sums
+    // and stores a slice of the rows).  A short persistent launch (under 3
+    // rounds of tiles, where the tail round is a large share) also splits
+    // below K = 4096, in parts of at least 5 units (so from K = 1280):
+    // measured A/B, C5 out-projection (M = 17776, N = K = 1920, 560 tiles)
+    // 128.7 us unsplit against 123.1 us in 3 parts (5 parts: no faster than
+    // none); 4352 x 7936 x 1024 (527 tiles) 75.2 us unsplit against 80.5 us
+    // in 2 parts of 4 units; at 6-8 rounds (C5 QKV, MLP-up, K = 1920) 2-4
+    // parts were no faster than none.
     const int64_t T = (int64_t)p.tiles_m * p.tiles_n, R = T % cus, units = (K + 127) / 128;
     const bool can_persist = a_kmajor && b_kmajor && T > cus && cus % kNumXcd == 0;
-    const int64_t min_units = T > R ? 32 : 2;
+    const int64_t min_units = T <= R ? 2 : (can_persist && T < 3 * cus ? 10 : 32);
     if (R > 0 && 2 * R <= cus && units >= min_units && (T - R) % kNumXcd == 0) {
       int64_t sp = cus / R;
       if (sp > units) sp = units;
+      if (T > R && units < 32 && sp > units / 5) sp = units / 5;
       if (sp > 8) sp = 8;
       if (can_persist) {
         const int64_t per_xcd = (R + kNumXcd - 1) / kNumXcd;  // tail tiles on the busiest XCD
@@ -510,6 +521,14 @@ int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
           // fallback hand-off; the results must not change.
           const char* sh = getenv("SF_TEST_XCD_SHIFT");
           p.xcd_shift = sh != nullptr ? (atoi(sh) & (kNumXcd - 1)) : 0;
+          // Test hook: SF_TEST_SPLIT_SPINS = n (0 .. kSplitArriveSpins) caps
+          // how long a part waits for the others; 0 leaves every slice to
+          // the last part.  The results must not change.
+          const char* sp_env = getenv("SF_TEST_SPLIT_SPINS");
+          if (sp_env != nullptr) {
+            const int n = atoi(sp_env);
+            p.arrive_spins = n < 0 ? 0 : (n > kSplitArriveSpins ? kSplitArriveSpins : n);
+          }
         }
       }
     }
@@ -537,7 +556,8 @@ void gemm_split_needs(const GemmPlan& plan, size_t* part_bytes, int* counters) {
   } else {
     const int nsplit = plan.p.tiles_m * plan.p.tiles_n - plan.p.full_tiles;
     *part_bytes = (size_t)nsplit * plan.p.split * (256u * 256u * 4u);
-    *counters = nsplit;
+    // persistent: three words per split tile (split_handoff_shared)
+    *counters = plan.p.persist > 0 ? 3 * nsplit : nsplit;
   }
 }
 

@@ -80,6 +80,10 @@ struct GemmParams {
   // production).  A test sets it to make every part see itself off its XCD
   // and take the agent-scope fallback of split_arrive_xcd.
   int xcd_shift;
+  // Most polls a part of a shared split sum waits for the other parts
+  // (kSplitArriveSpins in production).  A test sets 0 so that every part
+  // but the last gives up at once and the last sums every slice.
+  int arrive_spins;
 };
 
 // Split-tile arrival, called by one thread of a workgroup after every
@@ -128,6 +132,74 @@ __device__ __forceinline__ int split_arrive_xcd(int* counter, int parts, int xcd
   const int before = __hip_atomic_fetch_add(counter, off ? 0x10001 : 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if ((before & 0xffff) == parts - 1 && ((before >> 16) != 0 || off)) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   return before & 0xffff;
+}
+
+// Bounded waits of the shared split hand-off, in polls of the arrival word
+// (an agent-scope load plus s_sleep 1, about a microsecond each): how long a
+// part waits for the other parts to arrive, and how long the last part waits
+// for the others to claim their slices before it takes what is unclaimed.
+constexpr int kSplitArriveSpins = 256;
+constexpr int kSplitClaimSpins = 32;
+
+// Split hand-off with the final sum shared among the parts, for launches
+// whose parts of one tile are all resident at once (the persistent grid, one
+// workgroup per CU).  Called by one thread of each part after every thread's
+// partial stores completed (s_waitcnt vmcnt(0), workgroup barrier).  Three
+// words per split tile, all zero between launches:
+//   w[0] arrivals: bits 0-3 parts arrived, bits 4-7 those of them that ran
+//        off the XCD the launch intended (they release at agent scope, and
+//        the readers then acquire at agent scope, as in split_arrive_xcd);
+//   w[1] claimed slices: bit q set once some part has taken slice q;
+//   w[2] parts done with w[0] and w[1]; the part that completes it clears
+//        all three for the next launch (every other part has made its last
+//        access to them by then).
+// Slice q is the part's share of the final sum (the kernel maps it to rows).
+// A part waits for all arrivals (at most arrive_spins polls), then claims
+// its own slice; the last part to arrive waits (bounded) for the other
+// parts' claims and takes every slice still unclaimed, so a part whose wait
+// ran out loses nothing and every slice is summed by exactly one part.  Returns the bitmask of
+// slices this part sums (0: none).
+__device__ __forceinline__ int split_handoff_shared(int* w, int parts, int part, int xcd, int arrive_spins) {
+  const int xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20) & 15;  // HW_REG_XCC_ID[3:0]
+  const bool off = xcc != xcd;
+  if (off) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __builtin_amdgcn_s_waitcnt(0);
+  }
+  const int inc = off ? 0x11 : 0x01;
+  int v = __hip_atomic_fetch_add(&w[0], inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + inc;
+  const bool last = (v & 15) == parts;
+  bool seen = last;
+#pragma nounroll
+  for (int it = 0; !seen && it < arrive_spins; ++it) {
+    __builtin_amdgcn_s_sleep(1);
+    v = __hip_atomic_load(&w[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    seen = (v & 15) == parts;
+  }
+  int mine = 0;
+  if (seen) {
+    if (((v >> 4) & 15) != 0 || off) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    const int full = (1 << parts) - 1;
+    if (!last) {
+      const int old = __hip_atomic_fetch_or(&w[1], 1 << part, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      mine = ((old >> part) & 1) ? 0 : 1 << part;
+    } else {
+#pragma nounroll
+      for (int it = 0; it < kSplitClaimSpins; ++it) {
+        if ((__hip_atomic_load(&w[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) | (1 << part)) == full) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      const int old = __hip_atomic_fetch_or(&w[1], full, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      mine = full & ~old;
+    }
+  }
+  // Every access above has returned its value before this increment issues.
+  if (__hip_atomic_fetch_add(&w[2], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == parts - 1) {
+    __hip_atomic_store(&w[0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&w[1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&w[2], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return mine;
 }
 
 template <typename T> struct Mfma16;

@@ -59,7 +59,11 @@ static int launch16_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hi
         if (p.persist > 0) {
           if (p.K % 128 != 0 || p.persist % kNumXcd != 0 || gy != 1)
             return fail(SF_ERR_INVALID_ARG, "persistent 256x256 kernel: K %% 128, grid %% 8 and batch 1 required");
-          hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut, 2, true, true, true>), g, dim3(512), 0, st, p);
+          // a split tail shares its final sum among the parts (SHARED)
+          if (p.split > 0)
+            hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut, 2, true, true, true, true>), g, dim3(512), 0, st, p);
+          else
+            hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut, 2, true, true, true>), g, dim3(512), 0, st, p);
           break;
         }
       }

@@ -71,8 +71,10 @@
 // workgroup barrier after it frees stage 1 for the next job's second pair.
 // The split tail places every part of a tile on one XCD (tail tile t on XCD
 // t % 8, parts on consecutive workgroups of that XCD), so the partial-sum
-// hand-off goes through that XCD's L2 without write-back or invalidate
-// (split_arrive_xcd).
+// hand-off goes through that XCD's L2 without write-back or invalidate.  The
+// parts of a tile are resident together, so they share the final sum: each
+// sums and stores its own slice of the tile's rows (split_handoff_shared)
+// instead of one part reading every partial through one CU.
 #pragma once
 
 #include "gemm16.hpp"
@@ -130,10 +132,12 @@ constexpr int waitcnt_imm(int vm, int lgkm) {
 // exactly (one slice pair, e.g. attention scores Q.K^T at head size 64): a
 // single 64 KB stage, so two workgroups share a CU and one's stores overlap
 // the other's loads.
-template <typename TIn, typename TOut, int NSTAGE = 2, bool A_KM = true, bool B_KM = true, bool PERSIST = false>
+template <typename TIn, typename TOut, int NSTAGE = 2, bool A_KM = true, bool B_KM = true, bool PERSIST = false,
+          bool SHARED = false>
 __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   static_assert(NSTAGE == 1 || NSTAGE == 2, "one or two pair stages");
   static_assert(!PERSIST || (NSTAGE == 2 && A_KM && B_KM), "persistent tiles: pipelined NT kernel only");
+  static_assert(!SHARED || PERSIST, "a shared split sum needs the persistent grid");
   static_assert(NSTAGE == 2 || (A_KM && B_KM), "K == 64 stage: K-contiguous operands only");
   constexpr int BM = 256, BN = 256, BK = 32;
   constexpr int WM = 128, WN = 64, FM = WM / 16, FN = WN / 16;
@@ -442,13 +446,69 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   // register, and a value held across it would be spilled to scratch.
   const int elane = lane_id_fresh();
 
-  // ---- split tile: park the partial, the last part sums all of them ---------
+  // ---- split tile: park the partial, then sum the parts ----------------------
   // Partials move with plain 16-byte stores and loads.  Each thread waits
-  // for its own stores (vmcnt 0) before the workgroup barrier; the counter
-  // increment after it is an agent-scope release and acquire
-  // (split_arrive), so the part that sees count split - 1 reads every other
-  // part's data as written.
-  if (NSTAGE == 2 && part >= 0) {
+  // for its own stores (vmcnt 0) before the workgroup barrier.
+  // One workgroup per tile: the counter increment after the barrier is an
+  // agent-scope release and acquire (split_arrive), so the part that sees
+  // count split - 1 reads every other part's data as written, and sums all
+  // of them.
+  // Persistent with SHARED: all parts of a tile are resident together, so
+  // the final sum is shared (split_handoff_shared): slice q is the 16-row
+  // blocks j with j % split == q of every wave, each summed and stored by
+  // one part.  `own` holds the row blocks this part sums and stores.
+  // Persistent without SHARED: the last part sums all (split_arrive_xcd).
+  int own = (1 << FM) - 1;
+  if constexpr (SHARED) {
+    if (part >= 0) {
+      const int tid = wave * 64 + elane;
+      float* mine = p.ws + (size_t)(split_tile * p.split + part) * (FN * FM * 512 * 4);
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+          *reinterpret_cast<f32x4*>(mine + (size_t)((i * FM + j) * 512 + tid) * 4) = acc[i][j];
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      __shared__ int slices;
+      if (tid == 0)
+        slices = split_handoff_shared(p.counters + 3 * split_tile, p.split, part, (xcd + p.xcd_shift) & (kNumXcd - 1),
+                                      p.arrive_spins);
+      __syncthreads();
+      const int sl = slices;  // workgroup-uniform
+      if (sl == 0) return;
+      own = 0;
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+        if ((sl >> (j % p.split)) & 1) own |= 1 << j;
+      // Sum each owned block over the parts in part order (the same bits
+      // whichever part sums it), every part read back from the workspace.
+      // Blocks of other slices are zeroed: staged by the epilogue, never
+      // stored, and no accumulator stays live across the sums.
+      const float* all = p.ws + (size_t)split_tile * p.split * (FN * FM * 512 * 4) + (size_t)tid * 4;
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        if ((own >> j) & 1) {
+          f32x4 sum[FN];
+#pragma unroll
+          for (int i = 0; i < FN; ++i) sum[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int q = 0; q < p.split; ++q) {
+            f32x4 v[FN];
+#pragma unroll
+            for (int i = 0; i < FN; ++i)
+              v[i] = *reinterpret_cast<const f32x4*>(all + ((size_t)(q * FN + i) * FM + j) * 512 * 4);
+#pragma unroll
+            for (int i = 0; i < FN; ++i) sum[i] += v[i];
+          }
+#pragma unroll
+          for (int i = 0; i < FN; ++i) acc[i][j] = sum[i];
+        } else {
+#pragma unroll
+          for (int i = 0; i < FN; ++i) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+    }
+  } else if (NSTAGE == 2 && part >= 0) {
     const int tid = wave * 64 + elane;
     float* mine = p.ws + (size_t)(split_tile * p.split + part) * (FN * FM * 512 * 4);
 #pragma unroll
@@ -519,6 +579,7 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   }
   constexpr int LANES_ROW = WN * 2 / 16;
   constexpr int ROWS_I = 64 / LANES_ROW;
+  static_assert(16 % ROWS_I == 0, "a store's rows lie in one 16-row block");
   uint16_t* C = static_cast<uint16_t*>(p.C) + b * p.sC;
   const bool vec_ok = ((p.ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
   // Residual: read in the accumulator layout (4 consecutive columns of one
@@ -526,10 +587,19 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   // element of R is read in a pass before that pass stores it.
   const void* R = p.res != nullptr ? static_cast<const uint16_t*>(p.res) + b * p.sR : nullptr;
   const bool rvec = R != nullptr && res_vec_ok<TOut>(R, p.ldr);
+  // MASKED: a part of a shared split sum, which stores only its own row
+  // blocks; whole tiles compile without that test.
+  auto epilogue = [&](auto masked_c) {
+  constexpr bool MASKED = decltype(masked_c)::value;
   with_act(act, [&](auto act_c) {
   constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
   for (int ps = 0; ps < WM / ROWS_S; ++ps) {
+    // A part of a shared split sum skips passes without a row block of its
+    // own (workgroup-uniform); a workgroup barrier has already followed the
+    // main loop there.
+    if constexpr (MASKED)
+      if (((own >> (ps * (ROWS_S / 16))) & ((1 << (ROWS_S / 16)) - 1)) == 0) continue;
     // The staging region is private to this wave: only the first pass
     // waits for the other waves (their last fragment reads of the main loop
     // may touch it); later passes order this wave's own LDS accesses.
@@ -574,7 +644,9 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
       const int gm = m0 + wm * WM + ps * ROWS_S + r;
       const int gn = n0 + wn * WN + cl * 8;
       const u32x4 val = vals[rr];
-      if (gm < M) {
+      // row block of this store, the same for every lane: ROWS_I divides 16
+      const bool own_blk = !MASKED || ((own >> ((ps * ROWS_S + rr * ROWS_I) >> 4)) & 1);
+      if (own_blk && gm < M) {
         uint16_t* crow = C + (int64_t)gm * p.ldc;
         if (vec_ok && gn + 8 <= N) {
           __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(crow + gn));
@@ -587,6 +659,15 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
     }
   }
   });
+  };
+  if constexpr (SHARED) {
+    if (part >= 0)
+      epilogue(std::true_type{});
+    else
+      epilogue(std::false_type{});
+  } else {
+    epilogue(std::false_type{});
+  }
   if (!has_next) break;
   // every wave is done with the staging area (stage 1) before the next
   // tile's second pair is loaded into it; then group 1 drops half a step

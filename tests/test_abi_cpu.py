@@ -111,13 +111,21 @@ def test_dispatch_for_config_shapes():
     assert plan(M=4096, N=11008, ldc=11008).startswith("gemm nt 256x256 lds-dma")
     assert plan(M=17776, N=1920, K=7680, lda=7680, ldb=7680, ldc=1920).startswith("gemm nt 256x256 lds-dma")
     # C5 tails (560 / 1610 / 2100 tiles): persistent tiles (more tiles than
-    # CUs, last round at most half full); behind whole waves only K >= 4096
-    # splits the last wave (MLP-down); out-projection, QKV and MLP-up run it
-    # unsplit
+    # CUs, last round at most half full); behind whole waves K >= 4096
+    # splits the last wave (MLP-down), and so does K >= 1280 in a launch of
+    # under 3 rounds, in parts of at least 5 k-units (out-projection: 15
+    # units, 3 parts); QKV and MLP-up (6-8 rounds) run it unsplit
     assert plan(M=17776, N=1920, K=7680, lda=7680, ldb=7680, ldc=1920) \
         == "gemm nt 256x256 lds-dma 16-bit persistent split-tail 48x5"
     assert plan(M=17776, N=1920, K=1920, lda=1920, ldb=1920, ldc=1920) \
+        == "gemm nt 256x256 lds-dma 16-bit persistent split-tail 48x3"
+    # below 10 k-units a short launch stays unsplit
+    assert plan(M=17776, N=1920, K=1024, lda=1024, ldb=1024, ldc=1920) \
         == "gemm nt 256x256 lds-dma 16-bit persistent"
+    assert plan(M=4352, N=7936, K=1024, lda=1024, ldb=1024, ldc=7936) \
+        == "gemm nt 256x256 lds-dma 16-bit persistent"
+    assert plan(M=17776, N=1920, K=1280, lda=1280, ldb=1280, ldc=1920) \
+        == "gemm nt 256x256 lds-dma 16-bit persistent split-tail 48x2"
     assert plan(M=17776, N=5760, K=1920, lda=1920, ldb=1920, ldc=5760) \
         == "gemm nt 256x256 lds-dma 16-bit persistent"
     assert plan(M=17776, N=7680, K=1920, lda=1920, ldb=1920, ldc=7680) \

@@ -275,6 +275,7 @@ SPLIT_CASES = [
     (4352, 4096, 4096, None, False, "split-tail 16x8"),    # 272 tiles: 16 left over, 8 parts of 4 units
     (7900, 2800, 4352, "gelu", True, "split-tail 85x2"),  # 341 tiles: 85 left, 34 units in 2 parts (XCD packing)
     (17776, 1920, 7680, None, True, "split-tail 48x5"),   # C5 MLP-down shape
+    (17776, 1920, 1920, "gelu", True, "split-tail 48x3"),  # C5 out-projection: short launch, 5 units a part
     # persistent tiles without a split: 2 rounds + 15 tiles; two whole rounds
     (4352, 7936, 1024, "silu", True, "persistent"),
     (4096, 8192, 512, None, True, "persistent"),
@@ -311,11 +312,44 @@ def test_persistent_split_off_xcd_fallback():
     check_bound(y0[rows], y64, gemm_bound(y64, absprod, k, "bfloat16", None), "persistent split")
 
 
+def test_persistent_split_shared_sum_sweep():
+    """The parts of a persistent split tile share the final sum: each waits
+    (a bounded number of polls) for the others, claims its slice of the rows
+    and sums it; the last part to arrive takes every slice still unclaimed.
+    SF_TEST_SPLIT_SPINS=0 makes every part but the last give up at once, so
+    the last part sums every slice: the output must be bit-identical (same
+    partials, same part order), and the per-tile words must be back at zero
+    for the next launch with the normal wait."""
+    m, n, k = 4352, 4096, 4096
+    rng = np.random.default_rng(78)
+    x = rnd(rng, (m, k), 1.0, "bfloat16")
+    w = rnd(rng, (n, k), 1.0 / np.sqrt(k), "bfloat16")
+    b = rnd(rng, (n,), 0.5, "bfloat16")
+    gx, gw, gb = up(x, "bfloat16"), up(w, "bfloat16"), up(b, "bfloat16")
+    plan = cu().gemm_plan(1, m, n, k, 1, gx.data_ptr, k, 0, gw.data_ptr, k, 0, n, 0, gx.dtype)
+    assert plan.endswith("persistent split-tail 16x8"), plan
+    y0 = down(cu().dev_linear_forward(gx, gw, gb, "silu"))
+    os.environ["SF_TEST_SPLIT_SPINS"] = "0"
+    try:
+        y1 = down(cu().dev_linear_forward(gx, gw, gb, "silu"))
+        y2 = down(cu().dev_linear_forward(gx, gw, gb, "silu"))
+    finally:
+        del os.environ["SF_TEST_SPLIT_SPINS"]
+    y3 = down(cu().dev_linear_forward(gx, gw, gb, "silu"))
+    for y in (y1, y2, y3):
+        assert np.array_equal(y.view(np.uint32), y0.view(np.uint32)), "the last-part sweep changed the output"
+    rows = np.r_[0, 1000, m - 256, m - 129, m - 1]
+    y64 = ref.linear_f64(x[rows], w, b, "silu")
+    absprod = np.abs(x[rows].astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+    check_bound(y0[rows], y64, gemm_bound(y64, absprod, k, "bfloat16", "silu"), "shared split sum")
+
+
 @pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: "%dx%dx%d" % c[:3])
 def test_split_tail_linear(case):
     """The 256x256 NT kernel with its last partial wave of tiles split over k:
-    fp32 partials in a workspace, summed in part order by the last part
-    (persistent tiles: the parts of a tile on one XCD); and persistent tiles
+    fp32 partials in a workspace, summed in part order (one workgroup per
+    tile: by the last part; persistent tiles: the parts of a tile on one XCD,
+    each summing and storing its slice of the rows); and persistent tiles
     without a split.
     Two launches in a row check that the per-tile counters reset; sampled
     rows (including every split tile's rows) against fp64, checksums over all."""
