@@ -344,6 +344,57 @@ def test_persistent_split_shared_sum_sweep():
     check_bound(y0[rows], y64, gemm_bound(y64, absprod, k, "bfloat16", "silu"), "shared split sum")
 
 
+def test_shared_split_sum_beside_another_kernel():
+    """The shared split sum waits (bounded) for parts that are resident
+    together in a persistent grid.  A persistent GEMM on a second stream,
+    launched at the same time, holds CUs while the split launch runs, so some
+    parts may start late: their siblings' waits run out and the last part
+    sums the slices they left.  Either way both outputs must equal the ones
+    computed alone, bit for bit."""
+    so = ctypes.CDLL(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                                  "scaffolding_amd", "libsfgemm.so"))
+    I64, P = ctypes.c_int64, ctypes.c_void_p
+    rng = np.random.default_rng(79)
+    shapes = [(4352, 4096, 4096), (4096, 8192, 512)]  # split-tail 16x8; persistent, no split
+    ops = []
+    for (m, n, k), expect in zip(shapes, ("persistent split-tail 16x8", "persistent")):
+        gx = up(rnd(rng, (m, k), 1.0, "bfloat16"), "bfloat16")
+        gw = up(rnd(rng, (n, k), 1.0 / np.sqrt(k), "bfloat16"), "bfloat16")
+        plan = cu().gemm_plan(1, m, n, k, 1, gx.data_ptr, k, 0, gw.data_ptr, k, 0, n, 0, gx.dtype)
+        assert plan.endswith(expect), plan
+        ops.append((m, n, k, gx, gw, cu().empty((m, n), cu().BFLOAT16)))
+    cu().device_synchronize()
+    streams = []
+    for _ in range(2):
+        sp = ctypes.c_void_p()
+        assert so.sf_stream_create(ctypes.byref(sp)) == 0
+        streams.append(sp)
+
+    def gemm(i):
+        m, n, k, gx, gw, out = ops[i]
+        return so.sf_gemm(0, 1, I64(m), I64(n), I64(k), I64(1), P(gx.data_ptr), I64(k), I64(0), P(gw.data_ptr),
+                          I64(k), I64(0), P(out.data_ptr), I64(n), I64(0), 2, 2, ctypes.c_float(1.0), None, 0,
+                          streams[i])
+    try:
+        want = []
+        for i in range(2):
+            assert gemm(i) == 0 and so.sf_stream_synchronize(streams[i]) == 0
+            want.append(cu().gputensor_bits_to_numpy(ops[i][5]).copy())
+        for _ in range(30):
+            assert gemm(1) == 0
+            assert gemm(0) == 0
+        for sp in streams:
+            assert so.sf_stream_synchronize(sp) == 0
+        for i in range(2):
+            assert np.array_equal(cu().gputensor_bits_to_numpy(ops[i][5]), want[i]), "stream %d" % i
+        # the per-tile words are back at zero: a later launch alone still matches
+        assert gemm(0) == 0 and so.sf_stream_synchronize(streams[0]) == 0
+        assert np.array_equal(cu().gputensor_bits_to_numpy(ops[0][5]), want[0])
+    finally:
+        for sp in streams:
+            so.sf_stream_destroy(sp)
+
+
 @pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: "%dx%dx%d" % c[:3])
 def test_split_tail_linear(case):
     """The 256x256 NT kernel with its last partial wave of tiles split over k:
