@@ -191,15 +191,16 @@ int sf_gemm_plan(int transA, int transB,
 int sf_sum_dim(const void* x, void* out, int64_t outer, int64_t dim_size, int64_t inner,
                sf_dtype in_dtype, sf_dtype out_dtype, void* stream);
 
-/* Fused attention forward, head size D = 64:
+/* Fused attention forward, head size D in {8, 16, ..., 64}:
  *   O[b] = softmax(scale * Q[b] K[b]^T) V[b],   b in [0, batch),
- * Q[b] Sq x 64, K[b] and V[b] Sk x 64, O[b] Sq x 64, row strides ld*,
+ * Q[b] Sq x D, K[b] and V[b] Sk x D, O[b] Sq x D, row strides ld*,
  * batch strides stride* (elements), 16-bit dtype (F16 or BF16), fp32
  * accumulation and softmax.  One launch; the Sq x Sk scores never reach
  * memory.  Replaces the three-launch GPU path of
  * scaled_dot_product_attention (nn/functional.py:310-321: dev_batched_matmul_nt,
  * dev_muls, dev_softmax, dev_batched_matmul) when there is no mask and no
- * dropout.  Requires D == 64, 0 < scale < inf, 16-byte aligned rows and
+ * dropout.  Requires D a multiple of 8 up to 64 (other head sizes return
+ * SF_ERR_UNSUPPORTED), 0 < scale < inf, 16-byte aligned rows and
  * strides (SF_ERR_UNSUPPORTED otherwise: callers fall back to sf_gemm +
  * sf_softmax_rows).  Any Sk >= 1. */
 int sf_attention(const void* Q, int64_t ldq, int64_t strideQ,

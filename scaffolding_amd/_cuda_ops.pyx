@@ -1005,7 +1005,7 @@ cdef object _mha_strided(q, int64_t q_off, int64_t ldq, k, int64_t k_off, int64_
     cdef char* pv = <char*>_ptr(v) + v_off * es
     cdef char* po = <char*>_ptr(out)
     cdef int ret = SF_ERR_UNSUPPORTED
-    if sdt != SF_F32 and D == 64 and scale > 0:
+    if sdt != SF_F32 and 8 <= D <= 64 and D % 8 == 0 and scale > 0:
         with nogil:
             ret = sf_attention_heads(pq, ldq, Nq * ldq, D, pk, ldk, Sk * ldk, D, pv, ldv, Sk * ldv, D,
                                      po, C, Nq * C, D, B, H, Nq, Sk, D, scale, sdt, NULL)
@@ -1139,7 +1139,8 @@ def dev_scaled_dot_product_attention(q, k, v, scale=None):
     """softmax(scale * Q K^T) V  (reference GPU path nn/functional.py:310-321).
     q (..., Sq, D), k and v (..., Sk, D) with equal leading dims.  One fused
     launch (sf_attention: scores never reach memory) for 16-bit inputs with
-    D == 64 and a positive finite scale; otherwise the three-launch path."""
+    D a multiple of 8 up to 64 and a positive finite scale; otherwise the
+    three-launch path."""
     d = q.shape[-1]
     s = (1.0 / sqrt(<double>d)) if scale is None else float(scale)
     _same_dtype(q, k, 'dev_scaled_dot_product_attention')
@@ -1155,7 +1156,7 @@ def dev_scaled_dot_product_attention(q, k, v, scale=None):
     cdef int64_t batch = 1
     for e in q.shape[:-2]:
         batch *= e
-    if q.dtype == np.float32 or d != 64 or not (0.0 < s < 3.0e38):
+    if q.dtype == np.float32 or d < 8 or d > 64 or d % 8 != 0 or not (0.0 < s < 3.0e38):
         return dev_sdpa_unfused(q, k, v, scale)
     out = _alloc_like(tuple(q.shape), q.dtype, q.device_id)
     cdef int ret
@@ -1165,9 +1166,10 @@ def dev_scaled_dot_product_attention(q, k, v, scale=None):
     cdef void* po = _ptr(out)
     cdef sf_dtype dt = _sf_dtype(q.dtype)
     cdef float fs = s
+    cdef int64_t dh = d
     with nogil:
-        ret = sf_attention(pq, 64, sq * 64, pk, 64, sk * 64, pv, 64, sk * 64, po, 64, sq * 64,
-                           batch, sq, sk, 64, fs, dt, NULL)
+        ret = sf_attention(pq, dh, sq * dh, pk, dh, sk * dh, pv, dh, sk * dh, po, dh, sq * dh,
+                           batch, sq, sk, dh, fs, dt, NULL)
     _check_kernel(ret)
     return out
 

@@ -663,7 +663,8 @@ int sf_attention_heads(const void* Q, int64_t ldq, int64_t strideQ, int64_t head
   if (batch < 0 || heads < 0 || Sq < 0 || Sk < 0 || D < 0)
     return fail(SF_ERR_INVALID_ARG, "sf_attention: negative size");
   if (dtype == SF_F32) return fail(SF_ERR_UNSUPPORTED, "sf_attention: 16-bit dtypes only");
-  if (D != 64) return fail(SF_ERR_UNSUPPORTED, "sf_attention: head size %lld (64 only)", (long long)D);
+  if (D < 8 || D > 64 || D % 8 != 0)
+    return fail(SF_ERR_UNSUPPORTED, "sf_attention: head size %lld (multiples of 8 up to 64)", (long long)D);
   if (!(scale > 0.0f) || scale > 3.0e38f)
     return fail(SF_ERR_UNSUPPORTED, "sf_attention: scale %g (positive and finite only)", (double)scale);
   if (batch == 0 || heads == 0 || Sq == 0) return SF_OK;
@@ -691,6 +692,7 @@ int sf_attention_heads(const void* Q, int64_t ldq, int64_t strideQ, int64_t head
   a.sQ = strideQ; a.sK = strideK; a.sV = strideV; a.sO = strideO;
   a.hQ = headQ; a.hK = headK; a.hV = headV; a.hO = headO;
   a.batch = batch; a.heads = heads; a.Sq = Sq; a.Sk = Sk;
+  a.D = D;
   return launch_attention(a, scale, dtype, static_cast<hipStream_t>(stream));
 }
 

@@ -12,6 +12,7 @@ int launch_attention(const AttnShape& a, float scale, sf_dtype dt, hipStream_t s
   p.H = (int)a.heads;
   p.ldq = (int)a.ldq; p.ldk = (int)a.ldk; p.ldv = (int)a.ldv; p.ldo = (int)a.ldo;
   p.Sq = (int)a.Sq; p.Sk = (int)a.Sk;
+  p.D = (int)a.D;
   p.scale_log2e = scale * 1.4426950408889634f;
   const unsigned gx = (unsigned)((a.Sq + 255) / 256);
   const int64_t pairs = a.batch * a.heads;

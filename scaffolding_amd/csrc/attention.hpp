@@ -25,8 +25,10 @@
 // keys 4g..4g+3 and 16+4g..16+4g+3 of each 32-key chunk), and the V
 // fragment reads use the same key order, so P never moves between lanes.
 // The 2 GB score and probability tensors of the three-kernel path are never
-// written.  Requires head size 64, scale > 0 and 16-byte aligned rows; a
-// partial last key block is masked.  grid.y runs over (batch, head) pairs,
+// written.  Head size D a multiple of 8 up to 64: the tiles stay 64 wide,
+// d past D reads as zeros (adding nothing to Q K^T; O's columns there are
+// not stored).  Requires scale > 0 and 16-byte aligned rows; a partial last
+// key block is masked.  grid.y runs over (batch, head) pairs,
 // each with its own batch and head offsets, so Q/K/V can be read in place
 // from a packed [batch, S, 3 * heads * 64] projection and O written straight
 // into [batch, Sq, heads * 64] (no head split or merge copies).
@@ -47,6 +49,7 @@ struct AttnParams {
   int H;                       // heads per batch entry
   int ldq, ldk, ldv, ldo;      // row strides, elements
   int Sq, Sk;
+  int D;                       // head size: a multiple of 8, at most 64
   float scale_log2e;           // scale * log2(e), > 0
 };
 
@@ -80,9 +83,14 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
   const __amdgpu_buffer_rsrc_t rV =
       __builtin_amdgcn_make_buffer_rsrc((void*)Vb, (short)0, (int)((uint32_t)Sk * (uint32_t)p.ldv * 2u), 0x00020000);
   const int drow = wave * 16 + (lane >> 3);
-  const uint32_t dch = (uint32_t)(((lane & 7) ^ (lane >> 3)) * 16);
-  const uint32_t vk0 = (uint32_t)drow * (uint32_t)p.ldk * 2u + dch;
-  const uint32_t vv0 = (uint32_t)drow * (uint32_t)p.ldv * 2u + dch;
+  const int hch = (lane & 7) ^ (lane >> 3);  // this lane's 16-byte chunk (8 d) of its rows
+  const uint32_t dch = (uint32_t)(hch * 16);
+  // Head sizes below 64: chunks at or past D get an offset past the buffer's
+  // range (2^31 plus at most the block and row offsets, which stay below
+  // 2^31) and so read as zeros.
+  const bool dok = 8 * hch < p.D;
+  const uint32_t vk0 = dok ? (uint32_t)drow * (uint32_t)p.ldk * 2u + dch : 0x80000000u;
+  const uint32_t vv0 = dok ? (uint32_t)drow * (uint32_t)p.ldv * 2u + dch : 0x80000000u;
   const uint32_t k8 = 8u * (uint32_t)p.ldk * 2u, v8 = 8u * (uint32_t)p.ldv * 2u;
   // The block's row offset goes in the per-lane offset, not the scalar
   // offset: the buffer's range check covers only the per-lane offset (plus
@@ -108,8 +116,10 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
     int r = q0 + mb * 16 + (lane & 15);
     r = r < Sq ? r : Sq - 1;
 #pragma unroll
-    for (int kc = 0; kc < 2; ++kc)
-      qf[mb][kc] = *reinterpret_cast<const u32x4*>(Qb + (int64_t)r * p.ldq + kc * 32 + 8 * (lane >> 4));
+    for (int kc = 0; kc < 2; ++kc) {
+      const int d0 = kc * 32 + 8 * (lane >> 4);
+      qf[mb][kc] = d0 < p.D ? *reinterpret_cast<const u32x4*>(Qb + (int64_t)r * p.ldq + d0) : u32x4{0u, 0u, 0u, 0u};
+    }
   }
 
   f32x4 o[4][4], osum[4];
@@ -305,6 +315,7 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
         const int d = db * 16 + 4 * (lane >> 4);
+        if (d >= p.D) continue;  // columns past the head size (D % 8 == 0)
         const uint32_t lo = pack2<T>(o[mb][db][0] * inv, o[mb][db][1] * inv);
         const uint32_t hi = pack2<T>(o[mb][db][2] * inv, o[mb][db][3] * inv);
         *reinterpret_cast<u32x2*>(orow + d) = u32x2{lo, hi};

@@ -80,6 +80,7 @@ struct AttnShape {
   int64_t sQ, sK, sV, sO;
   int64_t hQ, hK, hV, hO;
   int64_t batch, heads, Sq, Sk;
+  int64_t D;  // head size: a multiple of 8, at most 64
 };
 int launch_attention(const AttnShape& a, float scale, sf_dtype dt, hipStream_t st);
 // Layer norm (rms = false: centred, gamma and beta, optional per-group

@@ -46,8 +46,9 @@ def softmax(input: Tensor, dim: int = -1, dtype=None) -> Tensor:
 def scaled_dot_product_attention(q: Tensor, k: Tensor, v: Tensor, attn_mask=None,
                                  dropout_p: float = 0.0, scale: float | None = None) -> Tensor:
     """softmax(scale * q k^T) v, scale defaulting to 1/sqrt(head size).
-    16-bit inputs with head size 64 run as one fused launch (sf_attention:
-    the scores never reach memory); other inputs take three launches: a
+    16-bit inputs with a head size that is a multiple of 8 up to 64 run as
+    one fused launch (sf_attention: the scores never reach memory); other
+    inputs take three launches: a
     strided-batched QK^T with the scale in its epilogue, a row softmax and
     a strided-batched PV.  The reference's GPU path (nn/functional.py:310-321)
     runs a Python loop of per-head SGEMMs, a scale pass, the softmax and a

@@ -87,7 +87,10 @@ int main() {
   unsetenv("SF_PLAN_CU_COUNT");
 
   // other entry points' validation
-  EXPECT(sf_attention(P(256), 64, 0, P(256), 64, 0, P(256), 64, 0, P(256), 64, 0, 1, 64, 64, 32, 1.f, SF_F16, NULL) ==
+  // head sizes: multiples of 8 up to 64 run fused; others are refused
+  EXPECT(sf_attention(P(256), 80, 0, P(256), 80, 0, P(256), 80, 0, P(256), 80, 0, 1, 64, 64, 72, 1.f, SF_F16, NULL) ==
+         SF_ERR_UNSUPPORTED);
+  EXPECT(sf_attention(P(256), 64, 0, P(256), 64, 0, P(256), 64, 0, P(256), 64, 0, 1, 64, 64, 36, 1.f, SF_F16, NULL) ==
          SF_ERR_UNSUPPORTED);
   EXPECT(sf_attention(P(256), 64, 0, P(256), 64, 0, P(256), 64, 0, P(256), 64, 0, 1, 64, 0, 64, 1.f, SF_F16, NULL) ==
          SF_ERR_INVALID_ARG);

@@ -92,8 +92,8 @@ def test_fused_attention_large_scores_and_leading_dims():
 @pytest.mark.parametrize("shape", [(2, 40, 100, 64), (1, 64, 64, 32), (1, 33, 128, 80)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_other_shapes(shape):
-    """Sk = 100 (fused, masked tail), head sizes 32 and 80 (three-launch
-    path)."""
+    """Sk = 100 (fused, masked tail), head size 32 (fused on 64-wide tiles)
+    and 80 (three-launch path)."""
     b, sq, sk, d = shape
     rng = np.random.default_rng(3)
     q = rnd(rng, (b, sq, d), 1.0, "bfloat16")
@@ -103,6 +103,45 @@ def test_other_shapes(shape):
     o = down(g.dev_scaled_dot_product_attention(up(q, "bfloat16"), up(k, "bfloat16"), up(v, "bfloat16"), None))
     o64 = sdpa64(q, k, v, 1.0 / np.sqrt(d))
     assert float(np.max(np.abs(o - o64))) <= bound(q, k, v, 1.0 / np.sqrt(d), "bfloat16", unfused=True)
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("d", [8, 16, 32, 48, 56])
+def test_fused_small_head_sizes_ignore_columns_past_d(dtype, d):
+    """Head sizes below 64 run fused on 64-wide tiles.  Q, K and V are stored
+    with row stride 64 and NaN in every column past D (inside the same
+    allocation), and O's columns past D hold a sentinel: the output must be
+    finite, match fp64 over the first D columns, and leave the sentinel
+    columns untouched (d past D is neither read nor written)."""
+    so = ctypes.CDLL(os.path.join(ROOT, "scaffolding_amd", "libsfgemm.so"))
+    I64, P = ctypes.c_int64, ctypes.c_void_p
+    b, sq, sk = 2, 130, 177
+    rng = np.random.default_rng(100 + d)
+    q = rnd(rng, (b, sq, d), 1.0, dtype)
+    k = rnd(rng, (b, sk, d), 1.0, dtype)
+    v = rnd(rng, (b, sk, d), 1.0, dtype)
+
+    def padded(a):
+        out = np.full(a.shape[:-1] + (64,), np.nan, np.float32)
+        out[..., :d] = a
+        return out
+    gq, gk, gv = up(padded(q), dtype), up(padded(k), dtype), up(padded(v), dtype)
+    go = up(np.full((b, sq, 64), 7.0, np.float32), dtype)
+    scale = 1.0 / np.sqrt(d)
+    rc = so.sf_attention(P(gq.data_ptr), I64(64), I64(sq * 64), P(gk.data_ptr), I64(64), I64(sk * 64),
+                         P(gv.data_ptr), I64(64), I64(sk * 64), P(go.data_ptr), I64(64), I64(sq * 64),
+                         I64(b), I64(sq), I64(sk), I64(d), ctypes.c_float(scale), 2 if dtype == "bfloat16" else 1,
+                         None)
+    assert rc == 0
+    cu().device_synchronize()
+    o = down(go)
+    assert np.all(o[..., d:] == 7.0), "columns past the head size were written"
+    assert np.all(np.isfinite(o[..., :d]))
+    o64 = sdpa64(q, k, v, scale)
+    assert float(np.max(np.abs(o[..., :d] - o64))) <= bound(q, k, v, scale, dtype)
+    # and through the tensor entry point (contiguous rows of D)
+    o2 = down(cu().dev_scaled_dot_product_attention(up(q, dtype), up(k, dtype), up(v, dtype), None))
+    assert float(np.max(np.abs(o2 - o64))) <= bound(q, k, v, scale, dtype)
 
 
 def test_abi_refusals():
@@ -118,7 +157,9 @@ def test_abi_refusals():
                                I64(1), I64(64), I64(sk), I64(d), ctypes.c_float(scale), dt, None)
     assert call() == 0
     assert call(sk=96) == 0  # a partial last key block is masked
-    assert call(d=32) == -3 and b"head size" in so.sf_last_error()
+    assert call(d=32) == 0  # head sizes below 64 run on 64-wide tiles
+    assert call(d=72) == -3 and b"head size" in so.sf_last_error()
+    assert call(d=36) == -3 and b"head size" in so.sf_last_error()
     assert call(scale=0.0) == -3 and b"scale" in so.sf_last_error()
     assert call(dt=0) == -3 and b"16-bit" in so.sf_last_error()
     assert call(ld=63) == -2

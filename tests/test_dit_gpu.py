@@ -228,6 +228,22 @@ def test_attention_packed_in_place(dtype, shape):
     assert float(np.max(np.abs(o - o64))) <= attn_bound(qkv, dtype, n)
 
 
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("shape", [(2, 100, 3, 32), (1, 129, 2, 16), (1, 70, 5, 48)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_attention_packed_small_head_sizes(dtype, shape):
+    """Packed projections with head sizes below 64 run fused in place (head
+    stride D, K and V at column offsets C and 2C)."""
+    bsz, n, heads, d = shape
+    c = heads * d
+    rng = np.random.default_rng(bsz + n + heads + d)
+    qkv = rnd(rng, (bsz, n, 3 * c), 1.0, dtype)
+    o = down(cu().dev_attention_packed(up(qkv, dtype), heads))
+    o64 = dit.mha_f64(qkv[..., :c], qkv[..., c:2 * c], qkv[..., 2 * c:], heads)
+    assert o.shape == (bsz, n, c)
+    assert float(np.max(np.abs(o - o64))) <= attn_bound(qkv, dtype, n)
+
+
 @pytest.mark.parametrize("sk", [1, 5, 63, 65, 100, 127, 200, 1000])
 def test_fused_attention_ragged_keys(sk):
     """Key counts that are not multiples of the 64-key block: the tail is
@@ -246,8 +262,9 @@ def test_fused_attention_ragged_keys(sk):
 @pytest.mark.parametrize("shape", [(2, 70, 33, 2, 64), (1, 40, 77, 4, 32), (2, 20, 9, 3, 40)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_multihead_attention(dtype, shape):
-    """q (B, N, C), k and v (B, S, C): fused for 16-bit D = 64, the strided
-    GEMM + softmax path for other head sizes and fp32."""
+    """q (B, N, C), k and v (B, S, C): fused for 16-bit head sizes that are
+    multiples of 8 up to 64 (64, 32, 40 here), the strided GEMM + softmax
+    path for fp32."""
     bsz, n, s, heads, d = shape
     c = heads * d
     rng = np.random.default_rng(n * s + heads)
@@ -255,7 +272,7 @@ def test_multihead_attention(dtype, shape):
     o = down(cu().dev_multihead_attention(up(q, dtype), up(k, dtype), up(v, dtype), heads))
     o64 = dit.mha_f64(q, k, v, heads)
     bound = attn_bound(v, dtype, s)
-    if dtype != "float32" and d != 64:  # the unfused path rounds the scores too
+    if dtype != "float32" and not (d % 8 == 0 and d <= 64):  # the unfused path rounds the scores too
         smax = float(np.max(np.abs(q.astype(np.float64)))) * float(np.max(np.abs(k.astype(np.float64)))) * d
         bound += 2 * {"float16": 2.0 ** -11, "bfloat16": 2.0 ** -8}[dtype] * smax / np.sqrt(d) * \
             float(np.max(np.abs(v)))
