@@ -13,10 +13,11 @@
 //      read from LDS (ds_read_b128, 128-byte lines, chunk h at slot
 //      h ^ (row & 7), conflict-free as in the GEMM kernels);
 //   2. keeps the softmax in the exp2 domain against a per-row reference m
-//      that is raised lazily: only when a score exceeds m + 8 does the wave
-//      reduce the row maxima across the four lanes sharing a row and scale
-//      O and the row sums by 2^(m_old - m_new), so P = 2^(S scale log2 e - m)
-//      stays <= 2^8 and the common path needs no cross-lane traffic;
+//      that is raised lazily: the exponents x = S scale log2 e - m are formed
+//      in place, and only when one exceeds 8 does the wave reduce the row
+//      maxima across the four lanes sharing a row, raise m and scale O and
+//      the row sums by 2^(m_old - m_new), so P = 2^x stays <= 2^8 and the
+//      common path needs no cross-lane traffic;
 //   3. packs P to 16 bits (v_cvt_pk) and adds P V into the 64 x 64 fp32 O
 //      accumulator (32 MFMAs, V fragments from ds_read_b64_tr_b16, gfx950's
 //      transposing LDS read) and P 1 into the row sums (8 MFMAs against a
@@ -131,7 +132,7 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
   }
   float mrow[4];
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) mrow[mb] = -INFINITY;
+  for (int mb = 0; mb < 4; ++mb) mrow[mb] = 0.f;  // set by the first key block
   const float sc = p.scale_log2e;
   // 16-bit 1.0 in both halves of every dword: the X fragment of a ones block.
   const uint32_t one2 = (uint32_t)Elem<T>::from_f32(1.0f) * 0x10001u;
@@ -214,14 +215,23 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
     }
 
     // ---- online softmax with lazy rescale --------------------------------
-    // Each lane checks its 16 scores of each row against the row's current
-    // reference m; only if some score exceeds m + THRESH (log2 units) does
-    // the wave reduce the row maxima across the four lanes of each row and
-    // rescale O and the row sums.  Otherwise 2^(s sc - m) <= 2^THRESH.
-    float lmax[4];
+    // x = s scale log2(e) - m in place (the exponent of P, one FMA per score);
+    // each lane checks its 16 values of each row against THRESH.  Only when
+    // some value exceeds it, and always in the first key block (which sets m
+    // from m = 0, with O and the sums still zero), does the wave reduce the
+    // row maxima across the four lanes of each row, raise m by dm, lower x
+    // by dm and scale O and the row sums by 2^-dm.  Otherwise P = 2^x <=
+    // 2^THRESH.  The maxima run on FMA results, which need no quieting of
+    // signalling NaNs (the MFMA outputs would), against a constant.
     bool need = false;
+    float lmx[4];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
+      const float nm = -mrow[mb];
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) s[mb][nb][q] = __builtin_fmaf(s[mb][nb][q], sc, nm);
       float mx = fmaxf(fmaxf(s[mb][0][0], s[mb][0][1]), s[mb][0][2]);
       mx = fmaxf(fmaxf(mx, s[mb][0][3]), s[mb][1][0]);
       mx = fmaxf(fmaxf(mx, s[mb][1][1]), s[mb][1][2]);
@@ -230,25 +240,33 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
       mx = fmaxf(fmaxf(mx, s[mb][2][3]), s[mb][3][0]);
       mx = fmaxf(fmaxf(mx, s[mb][3][1]), s[mb][3][2]);
       mx = fmaxf(mx, s[mb][3][3]);
-      lmax[mb] = mx * sc;
-      need |= lmax[mb] > mrow[mb] + THRESH;
+      lmx[mb] = mx;
+      need |= mx > THRESH;
     }
-    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+    if (j == 0 || __builtin_amdgcn_ballot_w64(need) != 0) {
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
-        float mx = lmax[mb];
+        float mx = lmx[mb];
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mnew = fmaxf(mrow[mb], mx);
-        const float corr = __builtin_amdgcn_exp2f(mrow[mb] - mnew);
-        mrow[mb] = mnew;
-        osum[mb] *= corr;
+        // the first block sets m to the row maximum (finite: every row has a
+        // valid key there); later blocks only raise it
+        const float dm = j == 0 ? mx : fmaxf(mx, 0.f);
+        mrow[mb] += dm;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) o[mb][db] *= corr;
+        for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) s[mb][nb][q] -= dm;
+        if (j > 0) {
+          const float corr = __builtin_amdgcn_exp2f(-dm);
+          osum[mb] *= corr;
+#pragma unroll
+          for (int db = 0; db < 4; ++db) o[mb][db] *= corr;
+        }
       }
     }
     // ---- P = 2^(S scale - m) packed to 16 bits, O += P V, row sums -------
-    // Row block mb's exponentials (VALU: 16 exp2, 16 FMAs, 8 conversions)
+    // Row block mb's exponentials (VALU: 16 exp2, 8 conversions)
     // are interleaved with the MFMAs of row block mb - 1 (8 for P V, 2 for
     // the row sums): the MFMA pipe and the VALU run side by side within
     // the wave instead of one after the other.
@@ -257,7 +275,6 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
     u32x4 pf[4][2];
     auto expo = [&](auto mb_c) {
       constexpr int MB = decltype(mb_c)::value;
-      const float nm = -mrow[MB];
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         uint32_t w[4];
@@ -265,8 +282,8 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
         for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
           for (int q2 = 0; q2 < 2; ++q2) {
-            const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[MB][2 * c + hh][2 * q2], sc, nm));
-            const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[MB][2 * c + hh][2 * q2 + 1], sc, nm));
+            const float e0 = __builtin_amdgcn_exp2f(s[MB][2 * c + hh][2 * q2]);
+            const float e1 = __builtin_amdgcn_exp2f(s[MB][2 * c + hh][2 * q2 + 1]);
             w[hh * 2 + q2] = pack2<T>(e0, e1);
           }
         pf[MB][c] = u32x4{w[0], w[1], w[2], w[3]};
