@@ -481,13 +481,16 @@ int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
     // one part summing all: 127 us unsplit against 130 us in 5 parts; K =
     // 7680 runs 453 us in 5 parts against 535 us unsplit, both persistent).
     //
-    // Persistent tiles (K-contiguous operands, more tiles than CUs, CU
-    // count a multiple of 8): one workgroup per CU walks its tiles, the
-    // next tile's first loads under the current tile's end.  Taken when the
-    // last round is at most half full or the tail is split; with a fuller
-    // last round the hardware's dynamic dispatch balances better (C5 QKV
-    // 1610 tiles 311 -> 301 us, MLP-up 2100 tiles 400 -> 387 us; C3 M = 4096
-    // 688 tiles 261 us one workgroup per tile against 270 us persistent).
+    // Persistent tiles (K-contiguous A: NT, or NN as in dX = dY W; more
+    // tiles than CUs, CU count a multiple of 8): one workgroup per CU walks
+    // its tiles, the next tile's first loads under the current tile's end.
+    // Taken when the last round is at most half full or the tail is split;
+    // with a fuller last round the hardware's dynamic dispatch balances
+    // better (C5 QKV 1610 tiles 311 -> 301 us, MLP-up 2100 tiles 400 -> 387
+    // us; C3 M = 4096 688 tiles 261 us one workgroup per tile against 270
+    // us persistent).  NN (C5 backward dX, A/B twice): QKV backward 0.763 ->
+    // 0.742 ms, out-projection 0.291 -> 0.282 ms, MLP-up and MLP-down
+    // within 1 %.
     // Its split tail packs each tile's parts onto one XCD, at most CUs / 8
     // parts per XCD, and shares the final sum among the parts (each sums
     // and stores a slice of the rows).  A short persistent launch (under 3
@@ -499,7 +502,7 @@ int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
     // in 2 parts of 4 units; at 6-8 rounds (C5 QKV, MLP-up, K = 1920) 2-4
     // parts were no faster than none.
     const int64_t T = (int64_t)p.tiles_m * p.tiles_n, R = T % cus, units = (K + 127) / 128;
-    const bool can_persist = a_kmajor && b_kmajor && T > cus && cus % kNumXcd == 0;
+    const bool can_persist = a_kmajor && T > cus && cus % kNumXcd == 0;  // NT, or NN (dX)
     const int64_t min_units = T <= R ? 2 : (can_persist && T < 3 * cus ? 10 : 32);
     if (R > 0 && 2 * R <= cus && units >= min_units && (T - R) % kNumXcd == 0) {
       int64_t sp = cus / R;

@@ -67,6 +67,17 @@ static int launch16_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hi
           break;
         }
       }
+      if constexpr (AKM && !KM) {  // NN (dX = dY W): persistent tiles as for NT
+        if (p.persist > 0) {
+          if (p.K % 128 != 0 || p.persist % kNumXcd != 0 || gy != 1)
+            return fail(SF_ERR_INVALID_ARG, "persistent 256x256 kernel: K %% 128, grid %% 8 and batch 1 required");
+          if (p.split > 0)
+            hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut, 2, true, false, true, true>), g, dim3(512), 0, st, p);
+          else
+            hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut, 2, true, false, true>), g, dim3(512), 0, st, p);
+          break;
+        }
+      }
       if (p.K % 128 != 0 && (AKM || KM))
         return fail(SF_ERR_INVALID_ARG, "the 256x256 LDS-DMA kernel needs K %% 128 == 0 with a K-contiguous operand");
       hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut, 2, AKM, KM>), g, dim3(512), 0, st, p);

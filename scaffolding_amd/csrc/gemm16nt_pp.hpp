@@ -60,7 +60,7 @@
 // 128 x 64 result through its own 16 KB of the stage arrays (64-row passes,
 // 144-byte pitch) and stores 128-byte row segments with 16-byte lanes.
 //
-// Persistent tiles (PERSIST, K-contiguous operands, batch 1): one
+// Persistent tiles (PERSIST, K-contiguous A, B either way, batch 1): one
 // workgroup per CU walks a list of jobs — whole tiles in rounds of
 // gridDim.x, then at most one part of a split tail tile.  The k-pair stream
 // runs on across jobs: in the last pair of a job, the even step loads the
@@ -136,7 +136,7 @@ template <typename TIn, typename TOut, int NSTAGE = 2, bool A_KM = true, bool B_
           bool SHARED = false>
 __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   static_assert(NSTAGE == 1 || NSTAGE == 2, "one or two pair stages");
-  static_assert(!PERSIST || (NSTAGE == 2 && A_KM && B_KM), "persistent tiles: pipelined NT kernel only");
+  static_assert(!PERSIST || (NSTAGE == 2 && A_KM), "persistent tiles: pipelined kernel, K-contiguous A");
   static_assert(!SHARED || PERSIST, "a shared split sum needs the persistent grid");
   static_assert(NSTAGE == 2 || (A_KM && B_KM), "K == 64 stage: K-contiguous operands only");
   constexpr int BM = 256, BN = 256, BK = 32;
@@ -283,17 +283,33 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   } else {
     vob[0] = ((uint32_t)mrow * (uint32_t)p.ldb + (uint32_t)(n0 + mch * 8)) * 2u;
   }
-  // The next job's row offsets (persistent kernel: K-contiguous operands).
-  // Only the persistent kernel re-points the offsets; the one-job kernels
-  // keep the straight-line set-up above (written through this lambda, the
-  // both-M/N-contiguous kernel spilled two offsets to scratch).
+  // The next job's offsets (persistent kernel: K-contiguous A; B either
+  // way).  Only the persistent kernel re-points the offsets; the one-job
+  // kernels keep the straight-line set-up above (written through this
+  // lambda, the both-M/N-contiguous kernel spilled two offsets to scratch).
+  // The lane's row and chunk indices are recomputed from a fresh lane id
+  // here, not kept live across the main loop (with an M/N-contiguous B
+  // they would spill).
   auto set_offsets = [&](int am0, int bn0) {
     if constexpr (PERSIST) {
+      const int fl = lane_id_fresh();
+      const int frow = wave * 32 + (fl >> 3);
+      const uint32_t fch = (uint32_t)(((fl & 7) ^ (fl >> 3)) * 16);
 #pragma unroll
       for (int i = 0; i < DMA_I; ++i) {
-        const int ga = am0 + drow + i * 8, gb = bn0 + drow + i * 8;
-        voa[i] = (uint32_t)(ga < M ? ga : M - 1) * (uint32_t)p.lda * 2u + dchunk_b;
-        vob[i] = (uint32_t)(gb < N ? gb : N - 1) * (uint32_t)p.ldb * 2u + dchunk_b;
+        const int ga = am0 + frow + i * 8;
+        voa[i] = (uint32_t)(ga < M ? ga : M - 1) * (uint32_t)p.lda * 2u + fch;
+      }
+      if constexpr (B_KM) {
+#pragma unroll
+        for (int i = 0; i < DMA_I; ++i) {
+          const int gb = bn0 + frow + i * 8;
+          vob[i] = (uint32_t)(gb < N ? gb : N - 1) * (uint32_t)p.ldb * 2u + fch;
+        }
+      } else {
+        const int fmrow = wave * 8 + (fl >> 3);
+        const int fmch = (fl & 7) ^ (2 * ((fmrow >> 1) & 1) + 4 * ((fmrow >> 3) & 1));
+        vob[0] = ((uint32_t)fmrow * (uint32_t)p.ldb + (uint32_t)(bn0 + fmch * 8)) * 2u;
       }
     }
   };

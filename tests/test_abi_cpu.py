@@ -180,6 +180,17 @@ def test_dispatch_for_config_shapes():
         == "gemm tn 256x256 lds-dma 16-bit split-tail 64x4"
     assert plan(transA=1, transB=0, ldb=4096) == "gemm tn 256x256 lds-dma 16-bit"
     assert plan(transA=0, transB=0, ldb=4096) == "gemm nn 256x256 lds-dma 16-bit"
+    # dX (NN) with more tiles than CUs: persistent tiles, split tails as NT
+    # (C5 QKV / out-projection / MLP-down dX shapes)
+    assert plan(transA=0, transB=0, M=17776, N=1920, K=5760, lda=5760, ldb=1920, ldc=1920) \
+        == "gemm nn 256x256 lds-dma 16-bit persistent split-tail 48x5"
+    assert plan(transA=0, transB=0, M=17776, N=1920, K=1920, lda=1920, ldb=1920, ldc=1920) \
+        == "gemm nn 256x256 lds-dma 16-bit persistent split-tail 48x3"
+    assert plan(transA=0, transB=0, M=17776, N=7680, K=1920, lda=1920, ldb=7680, ldc=7680) \
+        == "gemm nn 256x256 lds-dma 16-bit persistent"
+    # dW (TN) stays one workgroup per tile
+    assert plan(transA=1, transB=0, M=5760, N=1920, K=17776, lda=5760, ldb=1920, ldc=1920) \
+        == "gemm tn 256x256 lds-dma 16-bit"
     assert plan(transA=1, transB=1) == "gemm tt 256x256 lds-dma 16-bit"
     assert plan(transA=1, transB=0, ldb=4096, K=4000) == "gemm tn 256x256 lds-dma 16-bit"  # any K for TN
     assert plan(transA=0, transB=0, ldb=4096, K=4000) == "gemm tile 256x256 16-bit"  # K % 128 != 0

@@ -195,8 +195,11 @@ LDS_DMA_CASES = [
     ("float16", 0, 0, 1000, 1104, 128, 16, 0, "gemm nn 256x256 lds-dma"),
     ("bfloat16", 1, 0, 1000, 1104, 256, 16, 0, "gemm tn 256x256 lds-dma"),
     ("bfloat16", 1, 0, 4352, 4096, 4096, 1, 0, "gemm tn 256x256 lds-dma 16-bit split-tail 16x8"),
-    ("bfloat16", 0, 0, 4352, 4096, 4096, 1, 1, "gemm nn 256x256 lds-dma 16-bit split-tail 16x8"),
-    ("bfloat16", 0, 0, 2104, 8000, 512, 1, 3, "gemm nn 256x256 lds-dma"),
+    # NN with more tiles than CUs: persistent tiles (split tail with a shared
+    # final sum; unsplit with ragged edges; the C5 out-projection's dX shape)
+    ("bfloat16", 0, 0, 4352, 4096, 4096, 1, 1, "gemm nn 256x256 lds-dma 16-bit persistent split-tail 16x8"),
+    ("bfloat16", 0, 0, 2104, 8000, 512, 1, 3, "gemm nn 256x256 lds-dma 16-bit persistent"),
+    ("bfloat16", 0, 0, 17776, 1920, 1920, 1, 1, "gemm nn 256x256 lds-dma 16-bit persistent split-tail 48x3"),
     ("float16", 1, 0, 2104, 8000, 512, 1, 2, "gemm tn 256x256 lds-dma"),
     # weight-gradient shapes: few output tiles, long and ragged K (tokens)
     ("bfloat16", 1, 0, 1920, 1920, 4000, 1, 0, "gemm tn 256x256 lds-dma 16-bit split-tail 64x4"),
