@@ -222,3 +222,50 @@ def test_north_star_linear_bias_bf16_4096():
     rs64 = x.astype(np.float64) @ w.astype(np.float64).sum(axis=0) + b.astype(np.float64).sum()
     rs = yh.astype(np.float64).sum(axis=1)
     assert np.all(np.abs(rs - rs64) <= n * cfg.tol_16(k)), float(np.max(np.abs(rs - rs64)))
+
+
+def test_runtime_module_surface():
+    """``sf.cuda`` (reference cuda/__init__.py:45-303) and
+    ``sf.backends.cuda.matmul.allow_tf32`` (reference backends/cuda.py:20-35)
+    on the device: availability and properties, events timing a GEMM,
+    the caching allocator's live and pooled bytes as a tensor comes and
+    goes, and the tf32 flag (recorded, the fp32 GEMM bit-identical either
+    way)."""
+    assert sf.cuda.is_available() and sf.cuda.device_count() >= 1
+    sf.cuda.set_device(0)
+    assert sf.cuda.current_device() == 0
+    props = sf.cuda.get_device_properties(0)
+    assert props["arch"].startswith("gfx950") and props["multi_processor_count"] > 0
+    assert props["total_memory"] > (1 << 34)
+    assert isinstance(sf.cuda.get_device_name(0), str)
+
+    rng = np.random.default_rng(5)
+    a = dev(rng.standard_normal((1024, 1024), dtype=np.float32))
+    b = dev(rng.standard_normal((1024, 1024), dtype=np.float32))
+    e0, e1 = sf.cuda.Event(), sf.cuda.Event()
+    e0.record()
+    c = sf.matmul(a, b)
+    e1.record()
+    e1.synchronize()
+    assert 0.0 < e0.elapsed_time(e1) < 1000.0
+
+    sf.cuda.synchronize()
+    live0 = sf.cuda.memory_allocated()
+    t = dev(np.zeros((1024, 1024), np.float32))  # 4 MiB
+    assert sf.cuda.memory_allocated() >= live0 + (4 << 20)
+    pooled0 = sf.cuda.memory_stats()["pooled_bytes"]
+    del t
+    assert sf.cuda.memory_allocated() <= live0 + (1 << 20)
+    assert sf.cuda.memory_stats()["pooled_bytes"] >= pooled0 + (4 << 20)  # the freed block is pooled
+    sf.cuda.empty_cache()
+    assert sf.cuda.memory_stats()["pooled_bytes"] == 0
+
+    ref_bits = host(c).view(np.uint32).copy()
+    sf.backends.cuda.matmul.allow_tf32 = True
+    try:
+        assert sf.backends.cuda.matmul.allow_tf32 is True
+        c2 = sf.matmul(a, b)
+    finally:
+        sf.backends.cuda.matmul.allow_tf32 = False
+    assert sf.backends.cuda.matmul.allow_tf32 is False
+    assert np.array_equal(host(c2).view(np.uint32), ref_bits)
