@@ -200,6 +200,7 @@ LDS_DMA_CASES = [
     ("bfloat16", 0, 0, 4352, 4096, 4096, 1, 1, "gemm nn 256x256 lds-dma 16-bit persistent split-tail 16x8"),
     ("bfloat16", 0, 0, 2104, 8000, 512, 1, 3, "gemm nn 256x256 lds-dma 16-bit persistent"),
     ("bfloat16", 0, 0, 17776, 1920, 1920, 1, 1, "gemm nn 256x256 lds-dma 16-bit persistent split-tail 48x3"),
+    ("float16", 0, 0, 4352, 4096, 4096, 1, 2, "gemm nn 256x256 lds-dma 16-bit persistent split-tail 16x8"),
     ("float16", 1, 0, 2104, 8000, 512, 1, 2, "gemm tn 256x256 lds-dma"),
     # weight-gradient shapes: few output tiles, long and ragged K (tokens)
     ("bfloat16", 1, 0, 1920, 1920, 4000, 1, 0, "gemm tn 256x256 lds-dma 16-bit split-tail 64x4"),
