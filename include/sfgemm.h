@@ -202,7 +202,11 @@ int sf_sum_dim(const void* x, void* out, int64_t outer, int64_t dim_size, int64_
  * dropout.  Requires D a multiple of 8 up to 64 (other head sizes return
  * SF_ERR_UNSUPPORTED), 0 < scale < inf, 16-byte aligned rows and
  * strides (SF_ERR_UNSUPPORTED otherwise: callers fall back to sf_gemm +
- * sf_softmax_rows).  Any Sk >= 1. */
+ * sf_softmax_rows).  Any Sk >= 1.  When the last round of work items
+ * (256 query rows of one batch entry) would leave most of the GPU idle,
+ * those items are split over key ranges whose fp32 partials pass through
+ * the library's per-device workspace (as sf_sum_dim's do) and are merged
+ * by a second launch. */
 int sf_attention(const void* Q, int64_t ldq, int64_t strideQ,
                  const void* K, int64_t ldk, int64_t strideK,
                  const void* V, int64_t ldv, int64_t strideV,

@@ -696,7 +696,17 @@ int sf_attention_heads(const void* Q, int64_t ldq, int64_t strideQ, int64_t head
   a.hQ = headQ; a.hK = headK; a.hV = headV; a.hO = headO;
   a.batch = batch; a.heads = heads; a.Sq = Sq; a.Sk = Sk;
   a.D = D;
-  return launch_attention(a, scale, dtype, static_cast<hipStream_t>(stream));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const AttnSplit sp = attn_split_plan(a, cu_count_current());
+  if (sp.parts == 0) return launch_attention(a, scale, dtype, sp, nullptr, st);
+  float* ws = nullptr;
+  int* cnt = nullptr;
+  int rc = split_workspace_acquire((size_t)(sp.items - sp.full) * (size_t)sp.parts * kAttnPartBytes, 0, st, &ws,
+                                   &cnt);
+  if (rc != SF_OK) return rc;
+  rc = launch_attention(a, scale, dtype, sp, ws, st);
+  const int rc2 = split_workspace_release(st);
+  return rc != SF_OK ? rc : rc2;
 }
 
 int sf_attention(const void* Q, int64_t ldq, int64_t strideQ, const void* K, int64_t ldk, int64_t strideK,

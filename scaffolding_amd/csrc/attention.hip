@@ -1,10 +1,52 @@
 // attention.hip — launcher of the fused attention kernel (attention.hpp).
+#include <cstdlib>
+
 #include "sf_internal.hpp"
 #include "attention.hpp"
 
 namespace sf {
 
-int launch_attention(const AttnShape& a, float scale, sf_dtype dt, hipStream_t st) {
+AttnSplit attn_split_plan(const AttnShape& a, int cus) {
+  AttnSplit sp;
+  sp.items = a.batch * a.heads * ((a.Sq + 255) / 256);
+  sp.full = sp.items;
+  sp.parts = 0;
+  const int64_t nb = (a.Sk + 63) / 64;
+  // Two workgroups per CU, all equally long: the items past the last whole
+  // round of slots run alone.  When that round is at most half full, its
+  // items are split into P key ranges (P * items <= slots, at least 8 key
+  // blocks a part, at most 16 parts), so the round takes about 1/P of a
+  // workgroup's time plus the combine.  Measured at 17776 tokens: 30 heads
+  // (2100 items over 512 slots) 2.47 ms unsplit against 2.13 ms for 29.
+  const int64_t slots = 2 * (int64_t)cus;
+  const int64_t tail = sp.items % slots;
+  int64_t P = 0;
+  if (tail > 0 && 2 * tail <= slots) {
+    P = slots / tail;
+    if (P > 16) P = 16;
+    if (P > nb / 8) P = nb / 8;
+  }
+  // Test hook: SF_TEST_ATTN_PARTS = P (2 .. 16) splits every item into P
+  // key ranges (at most one a key block); the results must agree with the
+  // unsplit kernel to rounding.
+  const char* tp = getenv("SF_TEST_ATTN_PARTS");
+  if (tp != nullptr && atoi(tp) >= 2) {
+    P = atoi(tp) > 16 ? 16 : atoi(tp);
+    if (P > nb) P = nb;
+    if (P >= 2) {
+      sp.full = 0;
+      sp.parts = (int)P;
+    }
+    return sp;
+  }
+  if (P >= 2) {
+    sp.full = sp.items - tail;
+    sp.parts = (int)P;
+  }
+  return sp;
+}
+
+int launch_attention(const AttnShape& a, float scale, sf_dtype dt, const AttnSplit& sp, float* ws, hipStream_t st) {
   AttnParams p;
   p.Q = a.Q; p.K = a.K; p.V = a.V; p.O = a.O;
   p.sQ = a.sQ; p.sK = a.sK; p.sV = a.sV; p.sO = a.sO;
@@ -14,16 +56,33 @@ int launch_attention(const AttnShape& a, float scale, sf_dtype dt, hipStream_t s
   p.Sq = (int)a.Sq; p.Sk = (int)a.Sk;
   p.D = (int)a.D;
   p.scale_log2e = scale * 1.4426950408889634f;
-  const unsigned gx = (unsigned)((a.Sq + 255) / 256);
-  const int64_t pairs = a.batch * a.heads;
-  for (int64_t y0 = 0; y0 < pairs; y0 += 65535) {
-    const int64_t ny = (pairs - y0) < 65535 ? (pairs - y0) : 65535;
-    p.y0 = y0;
+  p.QB = (int)((a.Sq + 255) / 256);
+  p.full_items = sp.full;
+  p.parts = sp.parts;
+  p.ws = ws;
+  // One workgroup per whole item, then one per split part.
+  const int64_t split_items = sp.items - sp.full;
+  const int64_t wgs = sp.full + (sp.parts > 0 ? split_items * sp.parts : 0);
+  constexpr int64_t kChunk = int64_t(1) << 30;  // workgroups per launch (grid.x < 2^31)
+  for (int64_t i0 = 0; i0 < wgs; i0 += kChunk) {
+    const int64_t n = (wgs - i0) < kChunk ? (wgs - i0) : kChunk;
+    p.item0 = i0;
     if (dt == SF_F16)
-      hipLaunchKernelGGL((attn64_kernel<F16>), dim3(gx, (unsigned)ny), dim3(256), 0, st, p);
+      hipLaunchKernelGGL((attn64_kernel<F16>), dim3((unsigned)n), dim3(256), 0, st, p);
     else
-      hipLaunchKernelGGL((attn64_kernel<BF16>), dim3(gx, (unsigned)ny), dim3(256), 0, st, p);
+      hipLaunchKernelGGL((attn64_kernel<BF16>), dim3((unsigned)n), dim3(256), 0, st, p);
     const int rc = check_launch("attention");
+    if (rc != SF_OK) return rc;
+  }
+  if (sp.parts == 0) return SF_OK;
+  for (int64_t i0 = 0; i0 < split_items; i0 += kChunk) {
+    const int64_t n = (split_items - i0) < kChunk ? (split_items - i0) : kChunk;
+    p.item0 = i0;
+    if (dt == SF_F16)
+      hipLaunchKernelGGL((attn_combine_kernel<F16>), dim3((unsigned)n), dim3(256), 0, st, p);
+    else
+      hipLaunchKernelGGL((attn_combine_kernel<BF16>), dim3((unsigned)n), dim3(256), 0, st, p);
+    const int rc = check_launch("attention (combine)");
     if (rc != SF_OK) return rc;
   }
   return SF_OK;

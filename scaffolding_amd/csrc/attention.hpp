@@ -29,13 +29,24 @@
 // written.  Head size D a multiple of 8 up to 64: the tiles stay 64 wide,
 // d past D reads as zeros (adding nothing to Q K^T; O's columns there are
 // not stored).  Requires scale > 0 and 16-byte aligned rows; a partial last
-// key block is masked.  grid.y runs over (batch, head) pairs,
-// each with its own batch and head offsets, so Q/K/V can be read in place
-// from a packed [batch, S, 3 * heads * 64] projection and O written straight
-// into [batch, Sq, heads * 64] (no head split or merge copies).
+// key block is masked.  A work item is one (batch, head) pair's 256 query
+// rows, each pair with its own batch and head offsets, so Q/K/V can be read
+// in place from a packed [batch, S, 3 * heads * 64] projection and O written
+// straight into [batch, Sq, heads * 64] (no head split or merge copies).
+//
+// Split items.  Workgroups all run equally long, so when the last round of
+// them is short (items mod slots small) the launch waits a whole workgroup
+// time for a few of them.  The host then runs only the first full_items
+// whole and splits each remaining item's key blocks into `parts` contiguous
+// ranges, one workgroup each, dispatched after the whole items so they fill
+// the last round; such a workgroup writes its unnormalised fp32 O with its
+// row references m and row sums l (attn_part_* layout) and a second kernel,
+// attn_combine_kernel, merges the parts of each item in part order:
+// O = sum_p 2^(m_p - M) O_p / sum_p 2^(m_p - M) l_p, M = max_p m_p.
 #pragma once
 
 #include "gemm16nt_pp.hpp"
+#include "sf_internal.hpp"
 
 namespace sf {
 
@@ -46,7 +57,11 @@ struct AttnParams {
   void* O;
   int64_t sQ, sK, sV, sO;      // batch strides, elements
   int64_t hQ, hK, hV, hO;      // head strides, elements
-  int64_t y0;                  // first (batch, head) pair of this launch
+  int64_t item0;               // first work item (or split part) of this launch
+  int64_t full_items;          // items [0, full_items) run whole, the rest in parts
+  float* ws;                   // split parts' partials, kAttnPartFloats each
+  int QB;                      // query blocks of 256 rows per (batch, head) pair
+  int parts;                   // key-range parts per split item (0: none)
   int H;                       // heads per batch entry
   int ldq, ldk, ldv, ldo;      // row strides, elements
   int Sq, Sk;
@@ -55,6 +70,62 @@ struct AttnParams {
 };
 
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+// One split part's partials: O as [wave 4][row block 4][d block 4][lane 64]
+// f32x4 (the accumulator layout), then (m, l) as [wave 4][row block 4][lane
+// 64] float pairs.
+constexpr int kAttnPartOFloats = 4 * 4 * 4 * 64 * 4;
+constexpr int kAttnPartFloats = kAttnPartOFloats + 4 * 4 * 64 * 2;
+static_assert(kAttnPartFloats * 4 == (int)kAttnPartBytes, "partial layout and the host's size differ");
+
+// A work item's (pair, query block) and, for a split part, its key blocks.
+struct AttnItem {
+  int64_t b, h;
+  int qb;
+  int kb0, kb1;  // key blocks [kb0, kb1)
+  int64_t part;  // index of the split part among all parts, -1 for a whole item
+};
+__device__ __forceinline__ AttnItem attn_item(const AttnParams& p, int64_t it, int nb) {
+  AttnItem w;
+  int64_t item = it;
+  w.part = -1;
+  w.kb0 = 0;
+  w.kb1 = nb;
+  if (it >= p.full_items) {
+    const int64_t t = it - p.full_items;
+    const int64_t q = t / p.parts;
+    const int r = (int)(t - q * p.parts);
+    item = p.full_items + q;
+    w.part = t;
+    w.kb0 = (int)((int64_t)nb * r / p.parts);
+    w.kb1 = (int)((int64_t)nb * (r + 1) / p.parts);
+  }
+  const int64_t y = item / p.QB;
+  w.qb = (int)(item - y * p.QB);
+  w.b = y / p.H;
+  w.h = y - w.b * p.H;
+  return w;
+}
+
+// Normalised output rows of one wave: row block mb's 16 rows from the
+// accumulator layout (lane l: query l % 16, d = 16 db + 4 (l / 16) + 0..3),
+// columns at or past D not stored.
+template <typename T>
+__device__ __forceinline__ void attn_store_rows(const AttnParams& p, uint16_t* Ob, int q0, int lane, int mb,
+                                                const f32x4 (&o)[4], float l) {
+  const float inv = 1.0f / l;
+  const int r = q0 + mb * 16 + (lane & 15);
+  if (r >= p.Sq) return;
+  uint16_t* orow = Ob + (int64_t)r * p.ldo;
+#pragma unroll
+  for (int db = 0; db < 4; ++db) {
+    const int d = db * 16 + 4 * (lane >> 4);
+    if (d >= p.D) continue;  // columns past the head size (D % 8 == 0)
+    const uint32_t lo = pack2<T>(o[db][0] * inv, o[db][1] * inv);
+    const uint32_t hi = pack2<T>(o[db][2] * inv, o[db][3] * inv);
+    *reinterpret_cast<u32x2*>(orow + d) = u32x2{lo, hi};
+  }
+}
 
 template <typename T>
 __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
@@ -67,14 +138,15 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t y = p.y0 + blockIdx.y;
-  const int64_t b = y / p.H, h = y - b * p.H;
-  const int q0 = blockIdx.x * 256 + wave * 64;
   const int Sq = p.Sq, Sk = p.Sk;
   // Key blocks of 64; a partial last block reads zeros past row Sk (the
   // buffer bound) and its scores there are masked to -inf.
   const int NB = (Sk + KB - 1) / KB;
   const int k_tail = Sk - (NB - 1) * KB;  // valid keys of the last block, 1..64
+  const AttnItem wi = attn_item(p, p.item0 + blockIdx.x, NB);
+  const int64_t b = wi.b, h = wi.h;
+  const int q0 = wi.qb * 256 + wave * 64;
+  const int kb0 = wi.kb0, kb1 = wi.kb1;
   const uint16_t* Qb = static_cast<const uint16_t*>(p.Q) + b * p.sQ + h * p.hQ;
   const uint16_t* Kb = static_cast<const uint16_t*>(p.K) + b * p.sK + h * p.hK;
   const uint16_t* Vb = static_cast<const uint16_t*>(p.V) + b * p.sV + h * p.hV;
@@ -108,8 +180,8 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rV, (lds_ptr_t)(&sV[s][0] + wave * 2048 + 1024), 16, vv0 + v8 + vo, 0, 0,
                                              0);
   };
-  issue(0);
-  if (NB > 1) issue(1);
+  issue(kb0);
+  if (kb0 + 1 < kb1) issue(kb0 + 1);
 
   u32x4 qf[4][2];
 #pragma unroll
@@ -145,16 +217,16 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
   const int vch = (vs & 3) >> 1;
   const int vsw = vrow0 & 7;
 
-  for (int j = 0; j < NB; ++j) {
+  for (int j = kb0; j < kb1; ++j) {
     const int st = j % NS;
     __builtin_amdgcn_sched_barrier(0);
-    if (j + 1 < NB)
+    if (j + 1 < kb1)
       __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, 0));
     else
       __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    if (j + 2 < NB) issue(j + 2);
+    if (j + 2 < kb1) issue(j + 2);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- S = Q K^T, K fragments per 16-key block ------------------------
@@ -220,7 +292,8 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
     // some value exceeds it, and always in the first key block (which sets m
     // from m = 0, with O and the sums still zero), does the wave reduce the
     // row maxima across the four lanes of each row, raise m by dm, lower x
-    // by dm and scale O and the row sums by 2^-dm.  Otherwise P = 2^x <=
+    // by dm and scale O and the row sums by 2^-dm (the first key block of
+    // a split part likewise sets its own m).  Otherwise P = 2^x <=
     // 2^THRESH.  The maxima run on FMA results, which need no quieting of
     // signalling NaNs (the MFMA outputs would), against a constant.
     bool need = false;
@@ -243,7 +316,7 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
       lmx[mb] = mx;
       need |= mx > THRESH;
     }
-    if (j == 0 || __builtin_amdgcn_ballot_w64(need) != 0) {
+    if (j == kb0 || __builtin_amdgcn_ballot_w64(need) != 0) {
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
         float mx = lmx[mb];
@@ -251,13 +324,13 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         // the first block sets m to the row maximum (finite: every row has a
         // valid key there); later blocks only raise it
-        const float dm = j == 0 ? mx : fmaxf(mx, 0.f);
+        const float dm = j == kb0 ? mx : fmaxf(mx, 0.f);
         mrow[mb] += dm;
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
           for (int q = 0; q < 4; ++q) s[mb][nb][q] -= dm;
-        if (j > 0) {
+        if (j > kb0) {
           const float corr = __builtin_amdgcn_exp2f(-dm);
           osum[mb] *= corr;
 #pragma unroll
@@ -322,22 +395,54 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
     __builtin_amdgcn_sched_barrier(0);
   }
 
+  if (wi.part >= 0) {
+    // A split part: unnormalised O, m and l for attn_combine_kernel (rows
+    // past Sq too; the combine skips them).
+    float* wp = p.ws + wi.part * kAttnPartFloats;
+    f32x4* po = reinterpret_cast<f32x4*>(wp) + wave * 1024 + lane;
+    float2* pml = reinterpret_cast<float2*>(wp + kAttnPartOFloats) + wave * 256 + lane;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db) po[(mb * 4 + db) * 64] = o[mb][db];
+      pml[mb * 64] = float2{mrow[mb], osum[mb][0]};
+    }
+    return;
+  }
   uint16_t* Ob = static_cast<uint16_t*>(p.O) + b * p.sO + h * p.hO;
 #pragma unroll
+  for (int mb = 0; mb < 4; ++mb) attn_store_rows<T>(p, Ob, q0, lane, mb, o[mb], osum[mb][0]);
+}
+
+// Merges the parts of split items [full_items + item0 + blockIdx.x]: one
+// 256-thread workgroup per item, thread (wave, lane) reading the partials its
+// namesake wrote, in part order.
+template <typename T>
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t s = p.item0 + blockIdx.x;  // split item index
+  const AttnItem wi = attn_item(p, p.full_items + s * p.parts, 1);
+  const int q0 = wi.qb * 256 + wave * 64;
+  const float* base = p.ws + s * p.parts * (int64_t)kAttnPartFloats;
+  uint16_t* Ob = static_cast<uint16_t*>(p.O) + wi.b * p.sO + wi.h * p.hO;
   for (int mb = 0; mb < 4; ++mb) {
-    const float inv = 1.0f / osum[mb][0];
-    const int r = q0 + mb * 16 + (lane & 15);
-    if (r < Sq) {
-      uint16_t* orow = Ob + (int64_t)r * p.ldo;
+    const int ml_off = kAttnPartOFloats + ((wave * 4 + mb) * 64 + lane) * 2;
+    float mmax = -INFINITY;
+    for (int q = 0; q < p.parts; ++q) mmax = fmaxf(mmax, base[q * kAttnPartFloats + ml_off]);
+    float l = 0.f;
+    f32x4 o[4] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f},
+                  f32x4{0.f, 0.f, 0.f, 0.f}};
+    for (int q = 0; q < p.parts; ++q) {
+      const float* pq = base + q * kAttnPartFloats;
+      const float2 ml = *reinterpret_cast<const float2*>(pq + ml_off);
+      const float w = __builtin_amdgcn_exp2f(ml.x - mmax);
+      l += w * ml.y;
+      const f32x4* po = reinterpret_cast<const f32x4*>(pq) + (wave * 4 + mb) * 256 + lane;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const int d = db * 16 + 4 * (lane >> 4);
-        if (d >= p.D) continue;  // columns past the head size (D % 8 == 0)
-        const uint32_t lo = pack2<T>(o[mb][db][0] * inv, o[mb][db][1] * inv);
-        const uint32_t hi = pack2<T>(o[mb][db][2] * inv, o[mb][db][3] * inv);
-        *reinterpret_cast<u32x2*>(orow + d) = u32x2{lo, hi};
-      }
+      for (int db = 0; db < 4; ++db) o[db] += w * po[db * 64];
     }
+    attn_store_rows<T>(p, Ob, q0, lane, mb, o, l);
   }
 }
 

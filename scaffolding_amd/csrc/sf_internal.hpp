@@ -82,7 +82,18 @@ struct AttnShape {
   int64_t batch, heads, Sq, Sk;
   int64_t D;  // head size: a multiple of 8, at most 64
 };
-int launch_attention(const AttnShape& a, float scale, sf_dtype dt, hipStream_t st);
+// Work items of one attention call: (batch, head) pairs x blocks of 256
+// query rows.  Items [0, full) run whole; each later one is split into
+// `parts` key ranges (0: no split), whose fp32 partials take
+// kAttnPartBytes each in `ws` ((items - full) * parts of them).
+struct AttnSplit {
+  int64_t items;
+  int64_t full;
+  int parts;
+};
+constexpr size_t kAttnPartBytes = 73728;
+AttnSplit attn_split_plan(const AttnShape& a, int cus);
+int launch_attention(const AttnShape& a, float scale, sf_dtype dt, const AttnSplit& sp, float* ws, hipStream_t st);
 // Layer norm (rms = false: centred, gamma and beta, optional per-group
 // modulation y = h (1 + scale) + shift) or RMS norm (rms = true: gamma
 // only) over `rows` contiguous rows of `cols` elements.

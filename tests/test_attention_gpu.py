@@ -10,7 +10,7 @@ import os
 import numpy as np
 import pytest
 
-from helpers import cu, rnd, up
+from helpers import cu, quantize, rnd, up
 from oracle.configs import tol_16
 
 pytestmark = pytest.mark.gpu
@@ -164,6 +164,53 @@ def test_abi_refusals():
     assert call(dt=0) == -3 and b"16-bit" in so.sf_last_error()
     assert call(ld=63) == -2
     cu().device_synchronize()
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("parts", [2, 3, 16])
+@pytest.mark.parametrize("shape", [(2, 300, 1000, 64), (1, 513, 4095, 64), (3, 130, 1090, 32)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_split_key_ranges_match_fp64_and_unsplit(dtype, parts, shape, monkeypatch):
+    """Every work item split into `parts` key ranges (SF_TEST_ATTN_PARTS),
+    merged by the combine kernel: matches fp64 to the same bound as the
+    unsplit kernel, and the unsplit output to twice the output rounding
+    plus P's rounding.  One key far past the first part's range dominates
+    some rows, so the parts' row references m differ by large amounts and
+    the combine's weights 2^(m_p - M) span a wide range; Sk ragged (last
+    part masked), D = 32 (columns past D not stored)."""
+    b, sq, sk, d = shape
+    rng = np.random.default_rng(sq + sk + parts)
+    q = rnd(rng, (b, sq, d), 1.0, dtype)
+    k = rnd(rng, (b, sk, d), 1.0, dtype)
+    v = rnd(rng, (b, sk, d), 1.0, dtype)
+    k[:, sk - 70] = q[:, 0:8].mean(axis=1) * 5
+    k = quantize(k, dtype)
+    g = cu()
+    gq, gk, gv = up(q, dtype), up(k, dtype), up(v, dtype)
+    scale = 1.0 / np.sqrt(d)
+    monkeypatch.delenv("SF_TEST_ATTN_PARTS", raising=False)
+    o1 = down(g.dev_scaled_dot_product_attention(gq, gk, gv, scale))
+    monkeypatch.setenv("SF_TEST_ATTN_PARTS", str(parts))
+    o = down(g.dev_scaled_dot_product_attention(gq, gk, gv, scale))
+    monkeypatch.delenv("SF_TEST_ATTN_PARTS")
+    o64 = sdpa64(q, k, v, scale)
+    assert np.all(np.isfinite(o))
+    assert float(np.max(np.abs(o - o64))) <= bound(q, k, v, scale, dtype)
+    vmax = float(np.max(np.abs(v)))
+    assert float(np.max(np.abs(o - o1))) <= 4 * EPS[dtype] * vmax
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_split_plan_on_a_short_launch(dtype):
+    """One head, 1024 query rows, 2048 keys: 4 work items on 2 x CUs slots,
+    so the plan splits each into 4 key ranges of 8 blocks (no test hook)."""
+    rng = np.random.default_rng(21)
+    q = rnd(rng, (1, 1024, 64), 1.0, dtype)
+    k = rnd(rng, (1, 2048, 64), 1.0, dtype)
+    v = rnd(rng, (1, 2048, 64), 1.0, dtype)
+    g = cu()
+    o = down(g.dev_scaled_dot_product_attention(up(q, dtype), up(k, dtype), up(v, dtype), 0.125))
+    assert float(np.max(np.abs(o - sdpa64(q, k, v, 0.125)))) <= bound(q, k, v, 0.125, dtype)
 
 
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
