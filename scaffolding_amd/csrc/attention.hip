@@ -75,13 +75,13 @@ int launch_attention(const AttnShape& a, float scale, sf_dtype dt, const AttnSpl
     if (rc != SF_OK) return rc;
   }
   if (sp.parts == 0) return SF_OK;
-  for (int64_t i0 = 0; i0 < split_items; i0 += kChunk) {
-    const int64_t n = (split_items - i0) < kChunk ? (split_items - i0) : kChunk;
+  for (int64_t i0 = 0; i0 < split_items; i0 += kChunk / 16) {
+    const int64_t n = (split_items - i0) < kChunk / 16 ? (split_items - i0) : kChunk / 16;
     p.item0 = i0;
     if (dt == SF_F16)
-      hipLaunchKernelGGL((attn_combine_kernel<F16>), dim3((unsigned)n), dim3(256), 0, st, p);
+      hipLaunchKernelGGL((attn_combine_kernel<F16>), dim3((unsigned)(16 * n)), dim3(64), 0, st, p);
     else
-      hipLaunchKernelGGL((attn_combine_kernel<BF16>), dim3((unsigned)n), dim3(256), 0, st, p);
+      hipLaunchKernelGGL((attn_combine_kernel<BF16>), dim3((unsigned)(16 * n)), dim3(64), 0, st, p);
     const int rc = check_launch("attention (combine)");
     if (rc != SF_OK) return rc;
   }

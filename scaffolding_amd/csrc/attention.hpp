@@ -414,36 +414,41 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
   for (int mb = 0; mb < 4; ++mb) attn_store_rows<T>(p, Ob, q0, lane, mb, o[mb], osum[mb][0]);
 }
 
-// Merges the parts of split items [full_items + item0 + blockIdx.x]: one
-// 256-thread workgroup per item, thread (wave, lane) reading the partials its
-// namesake wrote, in part order.
+// Merges the parts of split items: one 64-thread workgroup per 16 query
+// rows (split item full_items + item0 + blockIdx.x / 16, wave w and row
+// block mb of it from blockIdx.x % 16), lane l reading the partials lane l
+// of that wave wrote, in part order.  Its time is load latency, not
+// bandwidth, so the part loops are unrolled to keep several loads in flight
+// and the grid has 16 workgroups per item.
 template <typename T>
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int64_t s = p.item0 + blockIdx.x;  // split item index
+__global__ __launch_bounds__(64) void attn_combine_kernel(AttnParams p) {
+  const int lane = threadIdx.x;
+  const int wave = (blockIdx.x >> 2) & 3;
+  const int mb = blockIdx.x & 3;
+  const int64_t s = p.item0 + (blockIdx.x >> 4);  // split item index
   const AttnItem wi = attn_item(p, p.full_items + s * p.parts, 1);
   const int q0 = wi.qb * 256 + wave * 64;
   const float* base = p.ws + s * p.parts * (int64_t)kAttnPartFloats;
   uint16_t* Ob = static_cast<uint16_t*>(p.O) + wi.b * p.sO + wi.h * p.hO;
-  for (int mb = 0; mb < 4; ++mb) {
-    const int ml_off = kAttnPartOFloats + ((wave * 4 + mb) * 64 + lane) * 2;
-    float mmax = -INFINITY;
-    for (int q = 0; q < p.parts; ++q) mmax = fmaxf(mmax, base[q * kAttnPartFloats + ml_off]);
-    float l = 0.f;
-    f32x4 o[4] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f},
-                  f32x4{0.f, 0.f, 0.f, 0.f}};
-    for (int q = 0; q < p.parts; ++q) {
-      const float* pq = base + q * kAttnPartFloats;
-      const float2 ml = *reinterpret_cast<const float2*>(pq + ml_off);
-      const float w = __builtin_amdgcn_exp2f(ml.x - mmax);
-      l += w * ml.y;
-      const f32x4* po = reinterpret_cast<const f32x4*>(pq) + (wave * 4 + mb) * 256 + lane;
+  const int ml_off = kAttnPartOFloats + ((wave * 4 + mb) * 64 + lane) * 2;
+  const int o_off = ((wave * 4 + mb) * 256 + lane) * 4;
+  float mmax = -INFINITY;
+#pragma unroll 8
+  for (int q = 0; q < p.parts; ++q) mmax = fmaxf(mmax, base[q * kAttnPartFloats + ml_off]);
+  float l = 0.f;
+  f32x4 o[4] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f},
+                f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll 4
+  for (int q = 0; q < p.parts; ++q) {
+    const float* pq = base + q * kAttnPartFloats;
+    const float2 ml = *reinterpret_cast<const float2*>(pq + ml_off);
+    const float w = __builtin_amdgcn_exp2f(ml.x - mmax);
+    l += w * ml.y;
+    const f32x4* po = reinterpret_cast<const f32x4*>(pq + o_off);
 #pragma unroll
-      for (int db = 0; db < 4; ++db) o[db] += w * po[db * 64];
-    }
-    attn_store_rows<T>(p, Ob, q0, lane, mb, o, l);
+    for (int db = 0; db < 4; ++db) o[db] += w * po[db * 64];
   }
+  attn_store_rows<T>(p, Ob, q0, lane, mb, o, l);
 }
 
 }  // namespace sf
