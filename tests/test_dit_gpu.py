@@ -244,6 +244,28 @@ def test_attention_packed_small_head_sizes(dtype, shape):
     assert float(np.max(np.abs(o - o64))) <= attn_bound(qkv, dtype, n)
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16"])
+def test_attention_packed_c5_shape_sampled_rows(dtype):
+    """The packed C5 shape itself (17776 tokens, 30 heads of 64): 2100 work
+    items of 256 query rows, 2048 run whole and the last 52 (head 29, rows
+    4608 onwards) as key-range parts merged by the combine launch.  Sampled
+    rows of whole and split items against fp64 over all 17776 keys."""
+    n, heads = 17776, 30
+    c = heads * 64
+    rng = np.random.default_rng(17776)
+    qkv = rnd(rng, (1, n, 3 * c), 1.0, dtype)
+    o = down(cu().dev_attention_packed(up(qkv, dtype), heads))
+    assert o.shape == (1, n, c)
+    rows = np.array([0, 1, 255, 4607, 4608, 4609, 9000, 12345, 17520, 17775])
+    for h in (0, 17, 28, 29):
+        q = qkv[:, rows, h * 64:(h + 1) * 64]
+        k = qkv[:, :, c + h * 64:c + (h + 1) * 64]
+        v = qkv[:, :, 2 * c + h * 64:2 * c + (h + 1) * 64]
+        o64 = ref.sdpa_f64(q, k, v, 0.125)
+        err = float(np.max(np.abs(o[:, rows, h * 64:(h + 1) * 64] - o64)))
+        assert err <= attn_bound(v, dtype, n), (h, err)
+
+
 @pytest.mark.parametrize("sk", [1, 5, 63, 65, 100, 127, 200, 1000])
 def test_fused_attention_ragged_keys(sk):
     """Key counts that are not multiples of the 64-key block: the tail is
