@@ -1,7 +1,7 @@
-// attention.hpp — fused scaled-dot-product attention forward for head size
-// 64, 16-bit Q/K/V/O with fp32 accumulation:
+// attention.hpp — fused scaled-dot-product attention forward for head sizes
+// up to 64, 16-bit Q/K/V/O with fp32 accumulation:
 //
-//   O[b] = softmax(scale * Q[b] K[b]^T) V[b],  Q [Sq, 64], K, V [Sk, 64].
+//   O[b] = softmax(scale * Q[b] K[b]^T) V[b],  Q [Sq, D], K, V [Sk, D].
 //
 // One 256-thread workgroup per 256 query rows of one batch entry; wave w
 // owns 64 of them (four 16-row blocks); at most 256 registers per lane, so
