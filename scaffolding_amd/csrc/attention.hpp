@@ -296,6 +296,44 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
     // a split part likewise sets its own m).  Otherwise P = 2^x <=
     // 2^THRESH.  The maxima run on FMA results, which need no quieting of
     // signalling NaNs (the MFMA outputs would), against a constant.
+    //
+    // fp16 (PCHECK): after the first key block the check runs on the packed
+    // P instead, three values per v_pk_maximum3_f16 (4 instructions per row
+    // block instead of 8 v_max3_f32): P > 2^THRESH (as 16-bit patterns,
+    // P >= 0) sends that row block through the same raise and recomputes
+    // its exponentials before its P V MFMAs.
+    constexpr bool PCHECK = std::is_same<T, F16>::value;
+    const bool first = j == kb0;
+    auto row_max = [&](int mb) {
+      float mx = fmaxf(fmaxf(s[mb][0][0], s[mb][0][1]), s[mb][0][2]);
+      mx = fmaxf(fmaxf(mx, s[mb][0][3]), s[mb][1][0]);
+      mx = fmaxf(fmaxf(mx, s[mb][1][1]), s[mb][1][2]);
+      mx = fmaxf(fmaxf(mx, s[mb][1][3]), s[mb][2][0]);
+      mx = fmaxf(fmaxf(mx, s[mb][2][1]), s[mb][2][2]);
+      mx = fmaxf(fmaxf(mx, s[mb][2][3]), s[mb][3][0]);
+      mx = fmaxf(fmaxf(mx, s[mb][3][1]), s[mb][3][2]);
+      return fmaxf(mx, s[mb][3][3]);
+    };
+    // Raises row block mb's reference by its row maxima (all four lanes of
+    // a row), lowers x, and scales O and the row sums.
+    auto raise = [&](int mb, float mx) {
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      // the first block sets m to the row maximum (finite: every row has a
+      // valid key there); later blocks only raise it
+      const float dm = first ? mx : fmaxf(mx, 0.f);
+      mrow[mb] += dm;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) s[mb][nb][q] -= dm;
+      if (!first) {
+        const float corr = __builtin_amdgcn_exp2f(-dm);
+        osum[mb] *= corr;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) o[mb][db] *= corr;
+      }
+    };
     bool need = false;
     float lmx[4];
 #pragma unroll
@@ -305,38 +343,14 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
       for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
         for (int q = 0; q < 4; ++q) s[mb][nb][q] = __builtin_fmaf(s[mb][nb][q], sc, nm);
-      float mx = fmaxf(fmaxf(s[mb][0][0], s[mb][0][1]), s[mb][0][2]);
-      mx = fmaxf(fmaxf(mx, s[mb][0][3]), s[mb][1][0]);
-      mx = fmaxf(fmaxf(mx, s[mb][1][1]), s[mb][1][2]);
-      mx = fmaxf(fmaxf(mx, s[mb][1][3]), s[mb][2][0]);
-      mx = fmaxf(fmaxf(mx, s[mb][2][1]), s[mb][2][2]);
-      mx = fmaxf(fmaxf(mx, s[mb][2][3]), s[mb][3][0]);
-      mx = fmaxf(fmaxf(mx, s[mb][3][1]), s[mb][3][2]);
-      mx = fmaxf(mx, s[mb][3][3]);
-      lmx[mb] = mx;
-      need |= mx > THRESH;
-    }
-    if (j == kb0 || __builtin_amdgcn_ballot_w64(need) != 0) {
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        float mx = lmx[mb];
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        // the first block sets m to the row maximum (finite: every row has a
-        // valid key there); later blocks only raise it
-        const float dm = j == kb0 ? mx : fmaxf(mx, 0.f);
-        mrow[mb] += dm;
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) s[mb][nb][q] -= dm;
-        if (j > kb0) {
-          const float corr = __builtin_amdgcn_exp2f(-dm);
-          osum[mb] *= corr;
-#pragma unroll
-          for (int db = 0; db < 4; ++db) o[mb][db] *= corr;
-        }
+      if (!PCHECK || first) {
+        lmx[mb] = row_max(mb);
+        need |= lmx[mb] > THRESH;
       }
+    }
+    if (first || (!PCHECK && __builtin_amdgcn_ballot_w64(need) != 0)) {
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) raise(mb, lmx[mb]);
     }
     // ---- P = 2^(S scale - m) packed to 16 bits, O += P V, row sums -------
     // Row block mb's exponentials (VALU: 16 exp2, 8 conversions)
@@ -371,7 +385,39 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
 #pragma unroll
       for (int db = 0; db < 4; ++db) o[MB][db] = Mfma16<T>::run(vf[db][1], pf[MB][1], o[MB][db]);
     };
+    // fp16 after the first key block: row block mb's packed P against
+    // 2^THRESH (0x5C00 = 256 in fp16; inf and NaN patterns exceed it); a
+    // row block that exceeds it is raised and its exponentials recomputed.
+    auto pcheck = [&](auto mb_c) {
+      constexpr int R = decltype(mb_c)::value;
+      if constexpr (PCHECK) {
+        if (!first) {
+          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+          h2 d[8];
+#pragma unroll
+          for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              // through a scalar: a bit cast of the vector element itself
+              // compiled to element 0 here
+              const uint32_t w = pf[R][c][e];
+              d[c * 4 + e] = __builtin_bit_cast(h2, w);
+            }
+          h2 m = __builtin_elementwise_maximum(__builtin_elementwise_maximum(d[0], d[1]), d[2]);
+          m = __builtin_elementwise_maximum(__builtin_elementwise_maximum(m, d[3]), d[4]);
+          m = __builtin_elementwise_maximum(__builtin_elementwise_maximum(m, d[5]), d[6]);
+          m = __builtin_elementwise_maximum(m, d[7]);
+          const uint32_t mb2 = __builtin_bit_cast(uint32_t, m);
+          const bool over = (mb2 & 0xffffu) > 0x5C00u || (mb2 >> 16) > 0x5C00u;
+          if (__builtin_amdgcn_ballot_w64(over) != 0) {
+            raise(R, row_max(R));
+            expo(mb_c);
+          }
+        }
+      }
+    };
     expo(std::integral_constant<int, 0>{});
+    pcheck(std::integral_constant<int, 0>{});
     __builtin_amdgcn_sched_barrier(0);
     // Raised wave priority for the P V stretch, so a SIMD's arbiter favours
     // the wave that is issuing MFMAs over its sibling (the other workgroup
@@ -389,6 +435,7 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
         __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
+      pcheck(std::integral_constant<int, I + 1>{});
     });
     pv(std::integral_constant<int, 3>{});
     __builtin_amdgcn_s_setprio(0);
