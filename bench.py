@@ -378,7 +378,15 @@ def cpu_baseline(budget_s: float = 20.0):
                       "warm-up, GC off, %d BLAS threads; %.3f s/trial" % (trials, threads, med),
             "ms_per_step": round(med * 1e3, 2),
             "cpu_model": _cpu_model(), "blas": _blas_name(),
+            "host_cpus": os.cpu_count(), "host_cpus_usable": _usable_cpus(),
             "single_thread": one}
+
+
+def _usable_cpus():
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return None
 
 
 def _cpu_model():

@@ -82,6 +82,19 @@ const char* sf_last_error(void);
 /* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
 int sf_version(void);
 
+/* Test hooks: force plans the planner would not pick; none of them may
+ * change a result.  No counterpart in the reference; for the library's own
+ * tests only (the library never reads them from the environment).
+ *   xcd_shift   0..7: each part of a persistent split tile expects the XCD
+ *               this many places from its own (0: off), so every part
+ *               takes the agent-scope fallback hand-off;
+ *   split_spins 0..256 caps how long a split part waits for the others
+ *               (0: the last part sums every slice); -1: the built-in bound;
+ *   attn_parts  0, or 2..16: split every fused-attention work item into
+ *               this many key ranges (at most 1 GiB of partials).
+ * Process-wide; SF_ERR_INVALID_ARG outside those ranges. */
+int sf_set_test_hooks(int xcd_shift, int split_spins, int attn_parts);
+
 /* ------------------------------------------------------------------ */
 /* GEMM family                                                         */
 /* ------------------------------------------------------------------ */
@@ -154,7 +167,12 @@ int sf_gemm_add(int transA, int transB,
  * SF_NOALLOC_SCRATCH_BYTES inside the library, which each GPU the library
  * runs on holds until the process ends; it calls no hipMalloc, hipFree or
  * other allocating routine.  A plan whose workspace exceeds the scratch
- * returns SF_ERR_UNSUPPORTED (no plan does on devices of up to 256 CUs).
+ * returns SF_ERR_UNSUPPORTED (no plan does on devices of up to 256 CUs,
+ * which covers every gfx950 part; on more CUs, tail splits of up to 256
+ * parts fit and larger ones are refused).  The first call on a device looks
+ * the scratch address up (hipGetSymbolAddress): under HIP graph capture,
+ * make one uncaptured call on that device first; the call itself launches
+ * kernels only (counters are cleared by a fill kernel, no memset node).
  * Every call on one device shares that device's scratch: calls that overlap
  * on one device (different streams, or host threads without ordering) race;
  * calls on one stream are ordered by it.  Asynchronous on `stream`. */
@@ -277,6 +295,28 @@ int sf_softmax_rows(const void* x, void* y, int64_t rows, int64_t cols,
                     sf_dtype in_dtype, sf_dtype out_dtype, float scale,
                     void* stream);
 
+/* Row softmax with an additive mask, the attn_mask of
+ * scaled_dot_product_attention (reference nn/functional.py:339-341:
+ * scores *= scale; scores += mask, NumPy broadcasting):
+ *   y[r, j] = softmax_j(scale * x[r, j] + mask[off(r) + j * stride_col]),
+ * r = b * rows_per_batch + i,
+ * off(r) = (b / inner_batches) * stride_outer + (b % inner_batches) * stride_inner
+ *          + i * stride_row.
+ * A zero stride broadcasts the mask over that axis; the batch index b of
+ * the scores' leading dims, flattened, splits into outer and inner groups
+ * (e.g. [B, H] scores with a [B, 1, Sq, Sk] mask: inner_batches = H,
+ * stride_inner = 0, stride_outer = Sq * Sk).  x and y are `dtype` (y == x
+ * allowed); the mask is `dtype` or F32, stride_col 0 or 1.  A row whose
+ * mask is -inf everywhere gives NaN, as the reference's NumPy does.  No
+ * counterpart in the reference's CUDA kernels (its masked SDPA runs on the
+ * host); asynchronous on `stream`. */
+int sf_softmax_rows_masked(const void* x, void* y, int64_t rows, int64_t cols,
+                           sf_dtype dtype, float scale,
+                           const void* mask, sf_dtype mask_dtype,
+                           int64_t rows_per_batch, int64_t inner_batches,
+                           int64_t stride_outer, int64_t stride_inner,
+                           int64_t stride_row, int64_t stride_col, void* stream);
+
 /* Standalone elementwise ops over n contiguous elements of dtype `dt`
  * (arithmetic in fp32, one rounding on store).  x == y is allowed.
  *   sf_silu  replaces cuda_silu_f32 (_cuda_kernels.cu:384)
@@ -329,6 +369,10 @@ int sf_cache_free(int device, void* ptr, size_t nbytes);
 int sf_cache_empty(int device);          /* device < 0: every device */
 int sf_cache_stats(int device, size_t* pooled_bytes, size_t* live_bytes);
 int sf_cache_set_limit(size_t bytes_per_device);
+/* Bytes of the per-device workspace that split plans (sf_gemm, sf_sum_dim,
+ * sf_attention) allocate on first use, on `device` (< 0: every device); 0
+ * before any such call.  Diagnostic, no reference counterpart. */
+int sf_workspace_bytes(int device, size_t* bytes);
 
 /* Copies; synchronous w.r.t. the host when stream is NULL. */
 int sf_memcpy_h2d(void* dst, const void* src, size_t nbytes, void* stream);

@@ -13,7 +13,7 @@ so the restatement below is the same sequence of NumPy calls:
   gelu (tanh)   0.5 x (1 + tanh(sqrt(2/pi)(x + 0.044715 x^3)))
                                                       reference nn/functional.py:79-82
   softmax       e = exp(x - max); e / sum(e)          reference nn/functional.py:137-141
-  sdpa          scores = q @ k^T; *= scale; softmax; @ v
+  sdpa          scores = q @ k^T; *= scale; += mask; softmax; @ v
                                                       reference nn/functional.py:323-357
   matmul_tn     np.matmul(a^T, b)                     reference autograd.py:296,813-818,
                                                       _mps_ops.pyx:279-298 (A^T @ B)
@@ -74,13 +74,18 @@ def softmax(x: np.ndarray, axis: int = -1) -> np.ndarray:
     return e
 
 
-def sdpa(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float | None = None) -> np.ndarray:
-    """reference nn/functional.py:323-357 without mask and dropout."""
+def sdpa(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float | None = None,
+         attn_mask: np.ndarray | None = None) -> np.ndarray:
+    """reference nn/functional.py:323-357 without dropout: the additive
+    attn_mask is added to the scaled scores with NumPy broadcasting
+    (:339-341) before the max-shifted softmax."""
     d = q.shape[-1]
     if scale is None:
         scale = 1.0 / math.sqrt(d)
     scores = np.matmul(q, np.swapaxes(k, -2, -1))
     scores *= scale
+    if attn_mask is not None:
+        scores += attn_mask
     s_max = scores.max(axis=-1, keepdims=True)
     scores -= s_max
     np.exp(scores, out=scores)
@@ -154,8 +159,11 @@ def softmax_f64(x, scale: float = 1.0) -> np.ndarray:
     return e / e.sum(axis=-1, keepdims=True)
 
 
-def sdpa_f64(q, k, v, scale: float) -> np.ndarray:
+def sdpa_f64(q, k, v, scale: float, attn_mask=None) -> np.ndarray:
     s = np.matmul(np.asarray(q, np.float64), np.swapaxes(np.asarray(k, np.float64), -2, -1))
+    if attn_mask is not None:
+        s = s * scale + np.asarray(attn_mask, np.float64)
+        return np.matmul(softmax_f64(s, 1.0), np.asarray(v, np.float64))
     return np.matmul(softmax_f64(s, scale), np.asarray(v, np.float64))
 
 

@@ -54,6 +54,7 @@ cdef extern from "sfgemm.h" nogil:
     const char* sf_status_string(int status)
     const char* sf_last_error()
     int sf_version()
+    int sf_set_test_hooks(int xcd_shift, int split_spins, int attn_parts)
 
     int sf_gemm(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_t batch,
                 const void* A, int64_t lda, int64_t strideA,
@@ -95,6 +96,11 @@ cdef extern from "sfgemm.h" nogil:
     int sf_add(const void* a, const void* b, void* y, int64_t n, sf_dtype dt, void* stream)
     int sf_softmax_rows(const void* x, void* y, int64_t rows, int64_t cols,
                         sf_dtype in_dtype, sf_dtype out_dtype, float scale, void* stream)
+    int sf_softmax_rows_masked(const void* x, void* y, int64_t rows, int64_t cols,
+                               sf_dtype dtype, float scale, const void* mask, sf_dtype mask_dtype,
+                               int64_t rows_per_batch, int64_t inner_batches,
+                               int64_t stride_outer, int64_t stride_inner,
+                               int64_t stride_row, int64_t stride_col, void* stream)
     int sf_silu(const void* x, void* y, int64_t n, sf_dtype dt, void* stream)
     int sf_gelu(const void* x, void* y, int64_t n, sf_dtype dt, void* stream)
     int sf_muls(const void* x, float s, void* y, int64_t n, sf_dtype dt, void* stream)
@@ -1123,24 +1129,111 @@ def dev_softmax(gt, int dim=-1, float scale=1.0):
     return out
 
 
-def dev_sdpa_unfused(q, k, v, scale=None):
-    """softmax(scale * Q K^T) V in three launches (QK^T with the scale folded
-    into its epilogue, row softmax, PV), scores kept in the input dtype:
-    the reference GPU path's structure (nn/functional.py:310-321)."""
+def _mask_layout(tuple mshape, tuple sshape):
+    """How a C-contiguous mask of shape `mshape` broadcasts (NumPy rules)
+    onto scores of shape `sshape` = (..., Sq, Sk): (rows_per_batch,
+    inner_batches, stride_outer, stride_inner, stride_row, stride_col) of
+    sf_softmax_rows_masked.  The scores' leading dims are merged into at
+    most two groups (outer, inner) of uniform mask stride; a mask that needs
+    more groups raises NotImplementedError."""
+    cdef int nd = len(sshape)
+    if nd < 1 or len(mshape) > nd:
+        raise ValueError("attn_mask of shape %s does not broadcast to scores %s" % (mshape, sshape))
+    ms = (1,) * (nd - len(mshape)) + tuple(mshape)
+    st = [0] * nd
+    acc = 1
+    for i in range(nd - 1, -1, -1):
+        st[i] = acc
+        acc *= ms[i]
+    eff = []
+    for i in range(nd):
+        if ms[i] == sshape[i]:
+            eff.append(st[i] if sshape[i] != 1 else 0)
+        elif ms[i] == 1:
+            eff.append(0)
+        else:
+            raise ValueError("attn_mask of shape %s does not broadcast to scores %s" % (mshape, sshape))
+    s_col = eff[nd - 1]
+    s_row = eff[nd - 2] if nd >= 2 else 0
+    per = sshape[nd - 2] if nd >= 2 else 1
+    merged = []
+    for i in range(nd - 2):
+        n, stv = sshape[i], eff[i]
+        if n == 1:
+            continue
+        if merged and merged[-1][1] == n * stv:
+            merged[-1] = (merged[-1][0] * n, stv)
+        else:
+            merged.append((n, stv))
+    if len(merged) > 2:
+        raise NotImplementedError("attn_mask of shape %s broadcasts over scores %s in more than two groups of "
+                                  "leading dims" % (mshape, sshape))
+    if not merged:
+        return per, 1, 0, 0, s_row, s_col
+    if len(merged) == 1:
+        return per, merged[0][0], 0, merged[0][1], s_row, s_col
+    return per, merged[1][0], merged[0][1], merged[1][1], s_row, s_col
+
+
+def dev_softmax_masked(scores, mask, float scale=1.0):
+    """softmax(scale * scores + mask) along the last dim, in place of the
+    reference's host branch scores *= scale; scores += mask; softmax
+    (nn/functional.py:337-347).  `mask` (a GpuTensor, or a host array that
+    is uploaded as fp32) broadcasts to the scores' shape with NumPy's rules;
+    additive, -inf entries allowed."""
+    if not isinstance(mask, GpuTensor):
+        mask = gputensor_from_numpy(np.ascontiguousarray(mask, dtype=np.float32), scores.device_id)
+    if mask.device_id != scores.device_id:
+        raise ValueError("dev_softmax_masked: the mask is on device %d, the scores on %d"
+                         % (mask.device_id, scores.device_id))
+    if mask.dtype != np.float32 and mask.dtype != scores.dtype:
+        mask = dev_cast(mask, np.float32)
+    sshape = tuple(scores.shape)
+    if len(sshape) == 0:
+        raise ValueError("dev_softmax_masked: scalar input")
+    per, inner, so, si, sr, sc = _mask_layout(tuple(mask.shape), sshape)
+    cdef int64_t cols = sshape[len(sshape) - 1]
+    cdef int64_t rows = scores.numel // cols if cols > 0 else 0
+    out = _alloc_like(sshape, scores.dtype, scores.device_id)
+    cdef sf_dtype dt = _sf_dtype(scores.dtype)
+    cdef sf_dtype mdt = _sf_dtype(mask.dtype)
+    cdef void* px = _ptr(scores)
+    cdef void* py = _ptr(out)
+    cdef void* pm = _ptr(mask)
+    cdef int64_t c_per = per, c_inner = inner, c_so = so, c_si = si, c_sr = sr, c_sc = sc
+    cdef int ret
+    with nogil:
+        ret = sf_softmax_rows_masked(px, py, rows, cols, dt, scale, pm, mdt, c_per, c_inner, c_so, c_si, c_sr,
+                                     c_sc, NULL)
+    _check_kernel(ret)
+    return out
+
+
+def dev_sdpa_unfused(q, k, v, scale=None, attn_mask=None):
+    """softmax(scale * Q K^T (+ attn_mask)) V in three launches (QK^T with
+    the scale folded into its epilogue, row softmax with the additive mask
+    folded in, PV), scores kept in the input dtype: the reference GPU path's
+    structure (nn/functional.py:310-321), with the mask of its host branch
+    (:339-341)."""
     d = q.shape[-1]
     s = (1.0 / sqrt(<double>d)) if scale is None else float(scale)
     scores = dev_batched_matmul_nt(q, k, s)
-    probs = dev_softmax(scores, -1)
+    if attn_mask is None:
+        probs = dev_softmax(scores, -1)
+    else:
+        probs = dev_softmax_masked(scores, attn_mask)
     del scores
     return dev_batched_matmul(probs, v)
 
 
-def dev_scaled_dot_product_attention(q, k, v, scale=None):
-    """softmax(scale * Q K^T) V  (reference GPU path nn/functional.py:310-321).
+def dev_scaled_dot_product_attention(q, k, v, scale=None, attn_mask=None):
+    """softmax(scale * Q K^T (+ attn_mask)) V  (reference GPU path
+    nn/functional.py:310-321; the mask as its host branch :339-341).
     q (..., Sq, D), k and v (..., Sk, D) with equal leading dims.  One fused
     launch (sf_attention: scores never reach memory) for 16-bit inputs with
-    D a multiple of 8 up to 64 and a positive finite scale; otherwise the
-    three-launch path."""
+    D a multiple of 8 up to 64, a positive finite scale and no mask;
+    otherwise, or when sf_attention declines the call
+    (SF_ERR_UNSUPPORTED), the three-launch path."""
     d = q.shape[-1]
     s = (1.0 / sqrt(<double>d)) if scale is None else float(scale)
     _same_dtype(q, k, 'dev_scaled_dot_product_attention')
@@ -1156,8 +1249,9 @@ def dev_scaled_dot_product_attention(q, k, v, scale=None):
     cdef int64_t batch = 1
     for e in q.shape[:-2]:
         batch *= e
-    if q.dtype == np.float32 or d < 8 or d > 64 or d % 8 != 0 or not (0.0 < s < 3.0e38):
-        return dev_sdpa_unfused(q, k, v, scale)
+    if attn_mask is not None or q.dtype == np.float32 or d < 8 or d > 64 or d % 8 != 0 \
+            or not (0.0 < s < 3.0e38):
+        return dev_sdpa_unfused(q, k, v, scale, attn_mask)
     out = _alloc_like(tuple(q.shape), q.dtype, q.device_id)
     cdef int ret
     cdef void* pq = _ptr(q)
@@ -1170,6 +1264,9 @@ def dev_scaled_dot_product_attention(q, k, v, scale=None):
     with nogil:
         ret = sf_attention(pq, dh, sq * dh, pk, dh, sk * dh, pv, dh, sk * dh, po, dh, sq * dh,
                            batch, sq, sk, dh, fs, dt, NULL)
+    if ret == SF_ERR_UNSUPPORTED:
+        del out
+        return dev_sdpa_unfused(q, k, v, scale)
     _check_kernel(ret)
     return out
 
@@ -1208,3 +1305,9 @@ def cuda_linear_forward(cnp.ndarray x not None, cnp.ndarray w not None, bias=Non
 
 def library_version():
     return sf_version()
+
+
+def _set_test_hooks(int xcd_shift=0, int split_spins=-1, int attn_parts=0):
+    """The library's test hooks (plans forced for tests; results unchanged).
+    Called with no arguments it turns them all off."""
+    _check_kernel(sf_set_test_hooks(xcd_shift, split_spins, attn_parts))

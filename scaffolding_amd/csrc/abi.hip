@@ -285,6 +285,8 @@ static int split_workspace_release(hipStream_t st) {
 static bool valid_dtype(int d) { return d == SF_F32 || d == SF_F16 || d == SF_BF16; }
 static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+TestHooks g_test_hooks;
+
 }  // namespace sf
 
 using namespace sf;
@@ -306,6 +308,19 @@ const char* sf_status_string(int status) {
 const char* sf_last_error(void) { return g_err; }
 
 int sf_version(void) { return 100; /* 0.1.0 */ }
+
+int sf_set_test_hooks(int xcd_shift, int split_spins, int attn_parts) {
+  if (xcd_shift < 0 || xcd_shift >= kNumXcd)
+    return fail(SF_ERR_INVALID_ARG, "sf_set_test_hooks: xcd_shift %d outside [0, %d)", xcd_shift, kNumXcd);
+  if (split_spins > kSplitArriveSpins)
+    return fail(SF_ERR_INVALID_ARG, "sf_set_test_hooks: split_spins %d above %d", split_spins, kSplitArriveSpins);
+  if (attn_parts != 0 && (attn_parts < 2 || attn_parts > 16))
+    return fail(SF_ERR_INVALID_ARG, "sf_set_test_hooks: attn_parts %d is neither 0 nor in [2, 16]", attn_parts);
+  g_test_hooks.xcd_shift.store(xcd_shift, std::memory_order_relaxed);
+  g_test_hooks.split_spins.store(split_spins < 0 ? -1 : split_spins, std::memory_order_relaxed);
+  g_test_hooks.attn_parts.store(attn_parts, std::memory_order_relaxed);
+  return SF_OK;
+}
 
 }  // extern "C"
 
@@ -519,19 +534,11 @@ int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
         p.split = (int)sp;
         if (can_persist) {
           p.persist = cus;
-          // Test hook: SF_TEST_XCD_SHIFT = s (1..7) makes every part expect
-          // the XCD s places away from its own, so each takes the agent-scope
-          // fallback hand-off; the results must not change.
-          const char* sh = getenv("SF_TEST_XCD_SHIFT");
-          p.xcd_shift = sh != nullptr ? (atoi(sh) & (kNumXcd - 1)) : 0;
-          // Test hook: SF_TEST_SPLIT_SPINS = n (0 .. kSplitArriveSpins) caps
-          // how long a part waits for the others; 0 leaves every slice to
-          // the last part.  The results must not change.
-          const char* sp_env = getenv("SF_TEST_SPLIT_SPINS");
-          if (sp_env != nullptr) {
-            const int n = atoi(sp_env);
-            p.arrive_spins = n < 0 ? 0 : (n > kSplitArriveSpins ? kSplitArriveSpins : n);
-          }
+          // Test hooks (sf_set_test_hooks): a forced XCD mismatch, a capped
+          // wait for the other parts.  Results must not change.
+          p.xcd_shift = g_test_hooks.xcd_shift.load(std::memory_order_relaxed) & (kNumXcd - 1);
+          const int spins = g_test_hooks.split_spins.load(std::memory_order_relaxed);
+          if (spins >= 0) p.arrive_spins = spins > kSplitArriveSpins ? kSplitArriveSpins : spins;
         }
       }
     }
@@ -806,6 +813,36 @@ int sf_softmax_rows(const void* x, void* y, int64_t rows, int64_t cols, sf_dtype
   return launch_softmax(x, y, rows, cols, in_dtype, out_dtype, scale, static_cast<hipStream_t>(stream));
 }
 
+int sf_softmax_rows_masked(const void* x, void* y, int64_t rows, int64_t cols, sf_dtype dtype, float scale,
+                           const void* mask, sf_dtype mask_dtype, int64_t rows_per_batch, int64_t inner_batches,
+                           int64_t stride_outer, int64_t stride_inner, int64_t stride_row, int64_t stride_col,
+                           void* stream) {
+  g_err[0] = 0;
+  if (!valid_dtype(dtype) || !valid_dtype(mask_dtype))
+    return fail(SF_ERR_INVALID_ARG, "sf_softmax_rows_masked: unknown dtype");
+  if (mask_dtype != dtype && mask_dtype != SF_F32)
+    return fail(SF_ERR_UNSUPPORTED, "sf_softmax_rows_masked: the mask's dtype must be the scores' dtype or F32");
+  if (rows < 0 || cols < 0) return fail(SF_ERR_INVALID_ARG, "sf_softmax_rows_masked: negative size");
+  if (rows > INT32_MAX || cols > INT32_MAX)
+    return fail(SF_ERR_INVALID_ARG, "sf_softmax_rows_masked: rows and cols must be < 2^31");
+  if (rows == 0 || cols == 0) return SF_OK;
+  if (x == nullptr || y == nullptr || mask == nullptr)
+    return fail(SF_ERR_INVALID_ARG, "sf_softmax_rows_masked: null pointer");
+  if (rows_per_batch < 1 || rows % rows_per_batch != 0 || inner_batches < 1)
+    return fail(SF_ERR_INVALID_ARG, "sf_softmax_rows_masked: rows_per_batch must divide rows, inner_batches >= 1");
+  if (stride_outer < 0 || stride_inner < 0 || stride_row < 0 || (stride_col != 0 && stride_col != 1))
+    return fail(SF_ERR_INVALID_ARG, "sf_softmax_rows_masked: negative mask stride, or stride_col not 0 or 1");
+  MaskArgs ma;
+  ma.m = mask;
+  ma.per = rows_per_batch;
+  ma.inner = inner_batches;
+  ma.souter = stride_outer;
+  ma.sinner = stride_inner;
+  ma.srow = stride_row;
+  ma.scol = (int)stride_col;
+  return launch_softmax_masked(x, y, rows, cols, dtype, scale, ma, mask_dtype, static_cast<hipStream_t>(stream));
+}
+
 static int unary_common(int op, const void* x, void* y, int64_t n, sf_dtype dt, float s,
                         void* stream, const char* name) {
   g_err[0] = 0;
@@ -1061,6 +1098,18 @@ int sf_cache_stats(int device, size_t* pooled_bytes, size_t* live_bytes) {
   }
   if (pooled_bytes) *pooled_bytes = pooled;
   if (live_bytes) *live_bytes = live;
+  return SF_OK;
+}
+
+int sf_workspace_bytes(int device, size_t* bytes) {
+  if (bytes == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_workspace_bytes: null pointer");
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  size_t total = 0;
+  for (auto& kv : g_ws) {
+    if (device >= 0 && kv.first != device) continue;
+    if (kv.second.base != nullptr) total += kv.second.part_bytes + (size_t)kv.second.counters * sizeof(int);
+  }
+  *bytes = total;
   return SF_OK;
 }
 

@@ -1,6 +1,4 @@
 // attention.hip — launcher of the fused attention kernel (attention.hpp).
-#include <cstdlib>
-
 #include "sf_internal.hpp"
 #include "attention.hpp"
 
@@ -26,18 +24,20 @@ AttnSplit attn_split_plan(const AttnShape& a, int cus) {
     if (P > 16) P = 16;
     if (P > nb / 8) P = nb / 8;
   }
-  // Test hook: SF_TEST_ATTN_PARTS = P (2 .. 16) splits every item into P
-  // key ranges (at most one a key block); the results must agree with the
-  // unsplit kernel to rounding.
-  const char* tp = getenv("SF_TEST_ATTN_PARTS");
-  if (tp != nullptr && atoi(tp) >= 2) {
-    P = atoi(tp) > 16 ? 16 : atoi(tp);
-    if (P > nb) P = nb;
-    if (P >= 2) {
+  // Test hook (sf_set_test_hooks): every item split into P key ranges (at
+  // most one a key block, and at most 1 GiB of partials); the results must
+  // agree with the unsplit kernel to rounding.
+  const int tp = g_test_hooks.attn_parts.load(std::memory_order_relaxed);
+  if (tp >= 2) {
+    int64_t hp = tp > 16 ? 16 : tp;
+    if (hp > nb) hp = nb;
+    const int64_t fit = (int64_t(1) << 30) / ((int64_t)kAttnPartBytes * sp.items);
+    if (hp > fit) hp = fit;
+    if (hp >= 2) {
       sp.full = 0;
-      sp.parts = (int)P;
+      sp.parts = (int)hp;
+      return sp;
     }
-    return sp;
   }
   if (P >= 2) {
     sp.full = sp.items - tail;

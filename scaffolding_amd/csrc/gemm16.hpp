@@ -193,7 +193,13 @@ __device__ __forceinline__ int split_handoff_shared(int* w, int parts, int part,
       mine = full & ~old;
     }
   }
-  // Every access above has returned its value before this increment issues.
+  // Every access above must have returned its value before this increment
+  // issues: a claim landing after the last part cleared w[1] would leave a
+  // stale bit for the next launch.  The w[2] increment has no data
+  // dependence on those accesses, so the order is enforced here: a compiler
+  // fence keeps the atomics in program order and the wait drains them.
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
   if (__hip_atomic_fetch_add(&w[2], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == parts - 1) {
     __hip_atomic_store(&w[0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(&w[1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

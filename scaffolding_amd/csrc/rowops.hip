@@ -90,6 +90,109 @@ __global__ __launch_bounds__(256) void softmax_block_kernel(const void* __restri
 }
 
 // ---------------------------------------------------------------------
+// Softmax with an additive mask (SDPA's attn_mask): y[r, :] =
+// softmax(scale * x[r, :] + mask_r), the mask of row r = b * per + i at
+// off(r) = (b / inner) * souter + (b % inner) * sinner + i * srow, element j
+// at off(r) + j * scol (scol 0: one value for the row).  Zero strides are
+// NumPy broadcasting over that axis.
+// ---------------------------------------------------------------------
+__device__ __forceinline__ int64_t mask_row_off(const MaskArgs& a, int64_t r) {
+  const int64_t b = r / a.per, i = r - b * a.per;
+  const int64_t bo = b / a.inner, bi = b - bo * a.inner;
+  return bo * a.souter + bi * a.sinner + i * a.srow;
+}
+
+// One wave per row, the row in registers (as softmax_wave_kernel); the
+// mask chunk loads beside the row's (scol 1: 16-byte aligned offsets).
+template <typename T, typename TM, int CPL>
+__global__ __launch_bounds__(256) void softmax_mask_wave_kernel(const void* __restrict__ x,
+                                                                void* __restrict__ y, int64_t rows,
+                                                                int cols, float scale, MaskArgs ma) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nch = cols >> 3;
+  const int64_t base = row * cols;
+  const int64_t mo = mask_row_off(ma, row);
+  const float mrow = ma.scol == 0 ? Chunk8<TM>::get(ma.m, mo) : 0.f;
+  float v[CPL][8];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = c * 64 + lane;
+    if (ch < nch) {
+      float mk[8];
+      Chunk8<T>::load(x, base + ch * 8, v[c]);
+      if (ma.scol != 0) {
+        Chunk8<TM>::load(ma.m, mo + ch * 8, mk);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mk[e] = mrow;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[c][e] = v[c][e] * scale + mk[e];
+        mx = fmaxf(mx, v[c][e]);
+      }
+    }
+  }
+  mx = wave_max(mx);
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = c * 64 + lane;
+    if (ch < nch) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[c][e] = fast_exp(v[c][e] - mx);
+        s += v[c][e];
+      }
+    }
+  }
+  s = wave_sum(s);
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = c * 64 + lane;
+    if (ch < nch) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[c][e] *= inv;
+      Chunk8<T>::store(y, base + ch * 8, v[c]);
+    }
+  }
+}
+
+// Any cols, strides or alignment: one block per row, three passes.
+template <typename T, typename TM>
+__global__ __launch_bounds__(256) void softmax_mask_block_kernel(const void* __restrict__ x,
+                                                                 void* __restrict__ y, int64_t rows,
+                                                                 int64_t cols, float scale, MaskArgs ma) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t base = row * cols;
+  const int64_t mo = mask_row_off(ma, row);
+  auto val = [&](int64_t c) {
+    return Chunk8<T>::get(x, base + c) * scale + Chunk8<TM>::get(ma.m, mo + c * ma.scol);
+  };
+  float mx = -INFINITY;
+  for (int64_t c = tid; c < cols; c += 256) mx = fmaxf(mx, val(c));
+  mx = wave_max(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float s = 0.f;
+  for (int64_t c = tid; c < cols; c += 256) s += fast_exp(val(c) - mx);
+  s = wave_sum(s);
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  s = red[0] + red[1] + red[2] + red[3];
+  const float inv = 1.0f / s;
+  for (int64_t c = tid; c < cols; c += 256) Chunk8<T>::put(y, base + c, fast_exp(val(c) - mx) * inv);
+}
+
+// ---------------------------------------------------------------------
 // Elementwise: y = f(x) over n elements, 8 per thread per iteration.
 // ---------------------------------------------------------------------
 enum UnaryOp { U_SILU = 0, U_GELU = 1, U_MULS = 2 };
@@ -351,6 +454,51 @@ int launch_softmax(const void* x, void* y, int64_t rows, int64_t cols, sf_dtype 
   else if (in == SF_F16) softmax_launch_i<F16>(out, x, y, rows, cols, scale, st);
   else softmax_launch_i<BF16>(out, x, y, rows, cols, scale, st);
   return check_launch("softmax");
+}
+
+template <typename T, typename TM>
+static void softmax_mask_launch_t(const void* x, void* y, int64_t rows, int64_t cols, float scale,
+                                  const MaskArgs& ma, hipStream_t st) {
+  const int64_t msz = (int64_t)sizeof(typename Elem<TM>::storage);
+  const bool mvec = ma.scol == 0 ||
+                    (aligned16(ma.m) && (ma.srow * msz) % 16 == 0 && (ma.souter * msz) % 16 == 0 &&
+                     (ma.sinner * msz) % 16 == 0);
+  if ((cols % 8 == 0) && aligned16(x) && aligned16(y) && cols <= 8192 && mvec) {
+    const unsigned grid = static_cast<unsigned>((rows + 3) / 4);
+    const int c = static_cast<int>(cols);
+    auto go = [&](auto cpl_c) {
+      constexpr int CPL = decltype(cpl_c)::value;
+      hipLaunchKernelGGL((softmax_mask_wave_kernel<T, TM, CPL>), dim3(grid), dim3(256), 0, st, x, y, rows, c,
+                         scale, ma);
+    };
+    if (cols <= 512)
+      go(std::integral_constant<int, 1>{});
+    else if (cols <= 1024)
+      go(std::integral_constant<int, 2>{});
+    else if (cols <= 2048)
+      go(std::integral_constant<int, 4>{});
+    else if (cols <= 4096)
+      go(std::integral_constant<int, 8>{});
+    else
+      go(std::integral_constant<int, 16>{});
+  } else {
+    hipLaunchKernelGGL((softmax_mask_block_kernel<T, TM>), dim3(static_cast<unsigned>(rows)), dim3(256), 0, st, x,
+                       y, rows, cols, scale, ma);
+  }
+}
+
+int launch_softmax_masked(const void* x, void* y, int64_t rows, int64_t cols, sf_dtype dt, float scale,
+                          const MaskArgs& ma, sf_dtype mask_dt, hipStream_t st) {
+  const bool mf32 = mask_dt == SF_F32;
+  if (dt == SF_F32) softmax_mask_launch_t<float, float>(x, y, rows, cols, scale, ma, st);
+  else if (dt == SF_F16) {
+    if (mf32) softmax_mask_launch_t<F16, float>(x, y, rows, cols, scale, ma, st);
+    else softmax_mask_launch_t<F16, F16>(x, y, rows, cols, scale, ma, st);
+  } else {
+    if (mf32) softmax_mask_launch_t<BF16, float>(x, y, rows, cols, scale, ma, st);
+    else softmax_mask_launch_t<BF16, BF16>(x, y, rows, cols, scale, ma, st);
+  }
+  return check_launch("softmax (masked)");
 }
 
 template <typename T>

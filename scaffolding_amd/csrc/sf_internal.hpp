@@ -4,6 +4,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include "gemm16.hpp"
 #include "sf_common.hpp"
 
@@ -15,6 +17,22 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int check_launch(const char* what);
 // Maps a HIP status to SF_OK / SF_ERR_HIP with context.
 int check_hip(hipError_t e, const char* what);
+
+// Test hooks, set only through sf_set_test_hooks (never read from the
+// environment): they force plans the planner would not pick, and every one
+// of them must leave results unchanged.
+//   xcd_shift   1..7: each part of a persistent split tile expects the XCD
+//               this many places from its own (the agent-scope fallback);
+//   split_spins >= 0: caps a split part's wait for the others (0: the last
+//               part sums every slice); < 0: the built-in bound;
+//   attn_parts  2..16: every attention work item split into this many key
+//               ranges; 0: the automatic plan.
+struct TestHooks {
+  std::atomic<int> xcd_shift{0};
+  std::atomic<int> split_spins{-1};
+  std::atomic<int> attn_parts{0};
+};
+extern TestHooks g_test_hooks;
 
 // Tile shapes of the 16-bit and fp32 GEMM kernels.
 enum TileCfg {
@@ -114,6 +132,15 @@ int launch_norm(const NormArgs& a, sf_dtype dt, hipStream_t st);
 int launch_add(const void* a, const void* b, void* y, int64_t n, sf_dtype dt, hipStream_t st);
 int launch_softmax(const void* x, void* y, int64_t rows, int64_t cols, sf_dtype in, sf_dtype out,
                    float scale, hipStream_t st);
+// Additive mask of a masked softmax (see sf_softmax_rows_masked).
+struct MaskArgs {
+  const void* m;
+  int64_t per, inner, souter, sinner, srow;
+  int scol;  // 0 or 1
+};
+// dt: scores in and probabilities out; mask_dt is dt or F32.
+int launch_softmax_masked(const void* x, void* y, int64_t rows, int64_t cols, sf_dtype dt, float scale,
+                          const MaskArgs& ma, sf_dtype mask_dt, hipStream_t st);
 int launch_unary(int op, const void* x, void* y, int64_t n, sf_dtype dt, float s, hipStream_t st);
 int launch_bias_rows(void* C, const void* bias, int64_t M, int64_t N, sf_dtype dt, hipStream_t st);
 int launch_cast(const void* x, sf_dtype in, void* y, sf_dtype out, int64_t n, hipStream_t st);

@@ -45,19 +45,31 @@ def softmax(input: Tensor, dim: int = -1, dtype=None) -> Tensor:
 
 def scaled_dot_product_attention(q: Tensor, k: Tensor, v: Tensor, attn_mask=None,
                                  dropout_p: float = 0.0, scale: float | None = None) -> Tensor:
-    """softmax(scale * q k^T) v, scale defaulting to 1/sqrt(head size).
-    16-bit inputs with a head size that is a multiple of 8 up to 64 run as
-    one fused launch (sf_attention: the scores never reach memory); other
-    inputs take three launches: a
-    strided-batched QK^T with the scale in its epilogue, a row softmax and
-    a strided-batched PV.  The reference's GPU path (nn/functional.py:310-321)
-    runs a Python loop of per-head SGEMMs, a scale pass, the softmax and a
-    batched SGEMM.  attn_mask and dropout are refused (NotImplementedError)."""
+    """softmax(scale * q k^T + attn_mask) v, scale defaulting to 1/sqrt(head
+    size).  16-bit inputs with a head size that is a multiple of 8 up to 64
+    and no mask run as one fused launch (sf_attention: the scores never
+    reach memory); other inputs take three launches: a strided-batched QK^T
+    with the scale in its epilogue, a row softmax with the additive mask
+    folded in, and a strided-batched PV.  The reference's GPU path
+    (nn/functional.py:310-321) runs a Python loop of per-head SGEMMs, a
+    scale pass, the softmax and a batched SGEMM, and sends a masked call to
+    its host branch (:339-341: scores += mask, NumPy broadcasting); here
+    the mask (a Tensor on the device, or a host array or CPU Tensor, which
+    is uploaded) is applied on the device with the same broadcasting.
+    dropout_p > 0 is refused (NotImplementedError): the reference's GPU
+    branch draws its own random mask (dev_dropout), which no result here
+    could reproduce."""
     if q._gpu is None or k._gpu is None or v._gpu is None:
         _gpu_only("scaled_dot_product_attention")
-    if attn_mask is not None or dropout_p > 0.0:
-        raise NotImplementedError("attn_mask / dropout are not on the device path")
+    if dropout_p > 0.0:
+        raise NotImplementedError("dropout is not on the device path")
+    mask = None
+    if attn_mask is not None:
+        if isinstance(attn_mask, Tensor):
+            mask = attn_mask._gpu if attn_mask._gpu is not None else attn_mask.numpy()
+        else:
+            mask = attn_mask
     d = q.shape[-1]
     s = (1.0 / math.sqrt(d)) if scale is None else float(scale)
-    out = _cuops.dev_scaled_dot_product_attention(q._gpu, k._gpu, v._gpu, s)
+    out = _cuops.dev_scaled_dot_product_attention(q._gpu, k._gpu, v._gpu, s, mask)
     return Tensor._wrap_gpu(out, q._device)

@@ -17,6 +17,9 @@ here independently of NumPy's BLAS:
                        adaptive scale / shift) and RMS norms, row by row in
                        math.fsum, and tiny single-head attentions (ragged
                        key counts) with fsum dot products and softmax sums
+  tiny_mask.npz        tiny attentions with an additive mask (reference
+                       nn/functional.py:339-341: scores * scale + mask,
+                       NumPy broadcasting, -inf entries) per row in fsum
   tiny_dit.npz         one tiny DiT block (self-attention, cross-attention
                        and the SiLU MLP, reference diffusion/models.py:538-590)
                        evaluated in pure Python lists with math.fsum: every
@@ -176,6 +179,43 @@ def tiny_norm():
     np.savez(os.path.join(HERE, "tiny_norm.npz"), **arrays)
 
 
+def tiny_mask():
+    """Masked attention over [B, H, Sq, Sk] = [2, 3, 4, 6] scores, d = 8,
+    with masks of four broadcast shapes; some entries -inf (never a whole
+    row).  Each output row: s_j = scale * fsum(q . k_j) + mask_j, then the
+    max-shifted exponentials and their fsum, per element."""
+    rng = np.random.default_rng(339)
+    b, h, sq, sk, d = 2, 3, 4, 6, 8
+    scale = 1.0 / math.sqrt(d)
+    arrays = {}
+    for name, mshape in [("qk", (sq, sk)), ("b1qk", (b, 1, sq, sk)), ("bh1k", (b, h, 1, sk)), ("1k", (1, sk))]:
+        q = rng.uniform(-2, 2, (b, h, sq, d))
+        k = rng.uniform(-2, 2, (b, h, sk, d))
+        v = rng.uniform(-1, 1, (b, h, sk, d))
+        mask = rng.uniform(-3, 3, mshape)
+        flat = mask.reshape(-1)
+        flat[rng.choice(flat.size, size=max(1, flat.size // 6), replace=False)] = -np.inf
+        # no row may be masked completely (that row would be NaN)
+        full = np.broadcast_to(mask, (b, h, sq, sk))
+        assert np.all(np.isfinite(full).any(axis=-1))
+        o = np.empty((b, h, sq, d))
+        for bi in range(b):
+            for hi in range(h):
+                for i in range(sq):
+                    qi = q[bi, hi, i].tolist()
+                    s = [scale * math.fsum(x * y for x, y in zip(qi, k[bi, hi, j].tolist())) + float(full[bi, hi, i, j])
+                         for j in range(sk)]
+                    m = max(s)
+                    e = [math.exp(t - m) for t in s]
+                    z = math.fsum(e)
+                    for dd in range(d):
+                        o[bi, hi, i, dd] = math.fsum(e[j] * float(v[bi, hi, j, dd]) for j in range(sk)) / z
+        key = "mask_" + name
+        arrays[key + "_q"], arrays[key + "_k"], arrays[key + "_v"] = q, k, v
+        arrays[key + "_mask"], arrays[key + "_o"] = mask, o
+    np.savez(os.path.join(HERE, "tiny_mask.npz"), **arrays)
+
+
 def tiny_dit():
     """B = 1, N = 3 tokens, C = 4 (2 heads of 2), cond_dim 3, context of 2
     tokens of width 5, MLP hidden 16."""
@@ -282,10 +322,9 @@ def config_inputs():
 
 
 if __name__ == "__main__":
-    tiny_gemm()
-    tiny_linear()
-    tiny_backward()
-    tiny_norm()
-    tiny_dit()
-    config_inputs()
+    # python tests/golden/make_golden.py [fixture ...]: all, or the named ones
+    makers = {"tiny_gemm": tiny_gemm, "tiny_linear": tiny_linear, "tiny_backward": tiny_backward,
+              "tiny_norm": tiny_norm, "tiny_mask": tiny_mask, "tiny_dit": tiny_dit, "config_inputs": config_inputs}
+    for name in sys.argv[1:] or list(makers):
+        makers[name]()
     print("fixtures written to", HERE)

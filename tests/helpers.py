@@ -59,14 +59,25 @@ def check_bound(y, y64, bound, what=""):
 
 
 def sample_rows(m: int, count: int, seed: int, tile: int = 256) -> np.ndarray:
-    """Row indices: tile edges, both ends, and a seeded random sample."""
-    edges = {0, 1, m - 1, m - 2}
-    for t in range(tile, m, tile):
-        edges.update({t - 1, t})
-    edges = sorted(e for e in edges if 0 <= e < m)
+    """Row indices: both ends, tile edges, the last (possibly ragged) tile,
+    and a seeded random sample.
+
+    Every tile edge pair (t - 1, t) is kept while there are at most 32 of
+    them; past that, 32 pairs evenly spaced over the tiles, the last tile's
+    always among them.  The last tile contributes its first two, middle and
+    last two rows, so a ragged tail is checked at any M."""
+    last = ((m - 1) // tile) * tile
+    keep = {0, 1, m - 2, m - 1, last - 1, last, last + 1, (last + m - 1) // 2}
+    starts = list(range(tile, m, tile))
+    if len(starts) > 32:
+        pick = np.unique(np.linspace(0, len(starts) - 1, 32).round().astype(np.int64))
+        starts = [starts[i] for i in pick]
+    for t in starts:
+        keep.update({t - 1, t})
+    edges = np.array(sorted(e for e in keep if 0 <= e < m), dtype=np.int64)
     rng = np.random.default_rng(seed)
     extra = rng.choice(m, size=min(count, m), replace=False)
-    return np.unique(np.concatenate([np.array(edges[:64], dtype=np.int64), extra]))
+    return np.unique(np.concatenate([edges, extra]))
 
 
 def rnd(rng, shape, std, dtype):

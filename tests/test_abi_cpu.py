@@ -76,6 +76,29 @@ def test_gemm_validation_without_device(lib, kw, code, text):
     assert text in lib.sf_last_error()
 
 
+@pytest.mark.parametrize("args,ok", [
+    ((0, -1, 0), True), ((3, 0, 16), True), ((7, 256, 2), True),
+    ((8, -1, 0), False), ((-1, -1, 0), False), ((0, 257, 0), False), ((0, -1, 1), False),
+    ((0, -1, 17), False),
+])
+def test_test_hooks_are_validated(lib, args, ok):
+    """The test hooks are set only through sf_set_test_hooks (the library
+    reads no environment variable for them) and are range-checked."""
+    try:
+        rc = lib.sf_set_test_hooks(*args)
+        assert (rc == 0) == ok, (args, rc)
+        if not ok:
+            assert rc == -2 and b"sf_set_test_hooks" in lib.sf_last_error()
+    finally:
+        assert lib.sf_set_test_hooks(0, -1, 0) == 0
+
+
+def test_library_reads_no_test_hook_from_the_environment():
+    src = "".join(open(os.path.join(ROOT, "scaffolding_amd", "csrc", f)).read()
+                  for f in os.listdir(os.path.join(ROOT, "scaffolding_amd", "csrc")))
+    assert "SF_TEST_" not in src
+
+
 def test_gemm_empty_is_noop(lib):
     assert gemm(lib, M=0, A=None, B=None, C=None) == 0
     assert gemm(lib, N=0, A=None, B=None, C=None) == 0

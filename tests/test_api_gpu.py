@@ -191,7 +191,7 @@ def test_sdpa_refusals_and_explicit_scale():
     rng = np.random.default_rng(6)
     q = rnd(rng, (2, 40, 64), 1.0, "bfloat16")
     tq = dev(q, "bfloat16")
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError, match="broadcast"):  # a (2, 40, 64) mask on (2, 40, 40) scores
         F.scaled_dot_product_attention(tq, tq, tq, attn_mask=tq)
     with pytest.raises(NotImplementedError):
         F.scaled_dot_product_attention(tq, tq, tq, dropout_p=0.1)

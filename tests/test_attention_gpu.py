@@ -170,8 +170,8 @@ def test_abi_refusals():
 @pytest.mark.parametrize("parts", [2, 3, 16])
 @pytest.mark.parametrize("shape", [(2, 300, 1000, 64), (1, 513, 4095, 64), (3, 130, 1090, 32)],
                          ids=lambda s: "x".join(map(str, s)))
-def test_split_key_ranges_match_fp64_and_unsplit(dtype, parts, shape, monkeypatch):
-    """Every work item split into `parts` key ranges (SF_TEST_ATTN_PARTS),
+def test_split_key_ranges_match_fp64_and_unsplit(dtype, parts, shape):
+    """Every work item split into `parts` key ranges (the attn_parts test hook),
     merged by the combine kernel: matches fp64 to the same bound as the
     unsplit kernel, and the unsplit output to twice the output rounding
     plus P's rounding.  One key far past the first part's range dominates
@@ -188,11 +188,12 @@ def test_split_key_ranges_match_fp64_and_unsplit(dtype, parts, shape, monkeypatc
     g = cu()
     gq, gk, gv = up(q, dtype), up(k, dtype), up(v, dtype)
     scale = 1.0 / np.sqrt(d)
-    monkeypatch.delenv("SF_TEST_ATTN_PARTS", raising=False)
     o1 = down(g.dev_scaled_dot_product_attention(gq, gk, gv, scale))
-    monkeypatch.setenv("SF_TEST_ATTN_PARTS", str(parts))
-    o = down(g.dev_scaled_dot_product_attention(gq, gk, gv, scale))
-    monkeypatch.delenv("SF_TEST_ATTN_PARTS")
+    g._set_test_hooks(attn_parts=parts)
+    try:
+        o = down(g.dev_scaled_dot_product_attention(gq, gk, gv, scale))
+    finally:
+        g._set_test_hooks()
     o64 = sdpa64(q, k, v, scale)
     assert np.all(np.isfinite(o))
     assert float(np.max(np.abs(o - o64))) <= bound(q, k, v, scale, dtype)

@@ -150,6 +150,9 @@ def test_c5_dit_projections_bf16(proj):
     assert gy.shape == (m, n)
     y = down(gy)
     rows = sample_rows(m, 192, seed=4 + k + n)
+    # the ragged last 256-row tile (17664..17775) is checked against fp64 too
+    last = (m - 1) // 256 * 256
+    assert np.count_nonzero(rows >= last) >= 4 and rows[-1] == m - 1
     y64 = ref.linear_f64(case.x[rows], case.w, case.b, case.act)
     err = _gate("C5 bf16 %s, abs vs fp64 (sampled rows)" % proj, cfg.abs_err(y[rows], y64), cfg.tol_16(k))
     assert err <= cfg.tol_16(k), err

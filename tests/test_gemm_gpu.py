@@ -286,7 +286,7 @@ def test_persistent_split_off_xcd_fallback():
     """The persistent split tail places every part of a tile on one XCD and
     hands partials over through that XCD's L2.  A part that finds itself on
     another XCD (hardware XCC_ID) releases at agent scope and makes the last
-    part acquire.  SF_TEST_XCD_SHIFT makes every part expect a different XCD,
+    part acquire.  The xcd_shift test hook makes every part expect a different XCD,
     so all of them take that fallback: the output must be bit-identical to
     the same-XCD hand-off (same parts, same summation order)."""
     m, n, k = 4352, 4096, 4096
@@ -297,12 +297,12 @@ def test_persistent_split_off_xcd_fallback():
     plan = cu().gemm_plan(1, m, n, k, 1, gx.data_ptr, k, 0, gw.data_ptr, k, 0, n, 0, gx.dtype)
     assert plan.endswith("persistent split-tail 16x8"), plan
     y0 = down(cu().dev_linear_forward(gx, gw, None))
-    os.environ["SF_TEST_XCD_SHIFT"] = "3"
+    cu()._set_test_hooks(xcd_shift=3)
     try:
         y1 = down(cu().dev_linear_forward(gx, gw, None))
         y2 = down(cu().dev_linear_forward(gx, gw, None))
     finally:
-        del os.environ["SF_TEST_XCD_SHIFT"]
+        cu()._set_test_hooks()
     y3 = down(cu().dev_linear_forward(gx, gw, None))
     for y in (y1, y2, y3):
         assert np.array_equal(y.view(np.uint32), y0.view(np.uint32)), "fallback hand-off changed the output"
@@ -316,7 +316,7 @@ def test_persistent_split_shared_sum_sweep():
     """The parts of a persistent split tile share the final sum: each waits
     (a bounded number of polls) for the others, claims its slice of the rows
     and sums it; the last part to arrive takes every slice still unclaimed.
-    SF_TEST_SPLIT_SPINS=0 makes every part but the last give up at once, so
+    The split_spins=0 test hook makes every part but the last give up at once, so
     the last part sums every slice: the output must be bit-identical (same
     partials, same part order), and the per-tile words must be back at zero
     for the next launch with the normal wait."""
@@ -329,12 +329,12 @@ def test_persistent_split_shared_sum_sweep():
     plan = cu().gemm_plan(1, m, n, k, 1, gx.data_ptr, k, 0, gw.data_ptr, k, 0, n, 0, gx.dtype)
     assert plan.endswith("persistent split-tail 16x8"), plan
     y0 = down(cu().dev_linear_forward(gx, gw, gb, "silu"))
-    os.environ["SF_TEST_SPLIT_SPINS"] = "0"
+    cu()._set_test_hooks(split_spins=0)
     try:
         y1 = down(cu().dev_linear_forward(gx, gw, gb, "silu"))
         y2 = down(cu().dev_linear_forward(gx, gw, gb, "silu"))
     finally:
-        del os.environ["SF_TEST_SPLIT_SPINS"]
+        cu()._set_test_hooks()
     y3 = down(cu().dev_linear_forward(gx, gw, gb, "silu"))
     for y in (y1, y2, y3):
         assert np.array_equal(y.view(np.uint32), y0.view(np.uint32)), "the last-part sweep changed the output"

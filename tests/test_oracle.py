@@ -238,6 +238,39 @@ def test_sdpa_known_answers():
     np.testing.assert_allclose(ref.sdpa(q, k0 + q, v, 0.7), ref.sdpa_f64(q, q, v, 0.7), rtol=1e-10, atol=1e-12)
 
 
+MASK_CASES = ["qk", "b1qk", "bh1k", "1k"]
+
+
+@pytest.mark.parametrize("name", MASK_CASES)
+def test_sdpa_mask_against_fsum_fixture(name):
+    """The additive mask (reference nn/functional.py:339-341) against the
+    fsum fixture, over four broadcast shapes with -inf entries; in fp32
+    (the reference's own restatement) and fp64."""
+    z = np.load(os.path.join(GOLDEN, "tiny_mask.npz"))
+    key = "mask_" + name
+    q, k, v, mask, o = (z[key + s] for s in ("_q", "_k", "_v", "_mask", "_o"))
+    scale = 1.0 / math.sqrt(q.shape[-1])
+    np.testing.assert_allclose(ref.sdpa_f64(q, k, v, scale, mask), o, rtol=1e-12, atol=1e-13)
+    got = ref.sdpa(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), None, mask.astype(np.float32))
+    np.testing.assert_allclose(got, o, rtol=2e-5, atol=2e-6)
+
+
+def test_sdpa_mask_planted_mistakes_fail():
+    """Plausible mistakes in applying the mask are caught by the fixture:
+    the mask ignored, added before the scale instead of after it, or only
+    its -inf entries applied (finite values dropped)."""
+    z = np.load(os.path.join(GOLDEN, "tiny_mask.npz"))
+    scale = 1.0 / math.sqrt(8)
+    for name in MASK_CASES:
+        key = "mask_" + name
+        q, k, v, mask, o = (z[key + s] for s in ("_q", "_k", "_v", "_mask", "_o"))
+        s = q @ np.swapaxes(k, -2, -1)
+        wrong = [ref.sdpa_f64(q, k, v, scale), ref.softmax_f64(s + mask, scale) @ v,
+                 ref.sdpa_f64(q, k, v, scale, np.where(np.isfinite(mask), 0.0, mask))]
+        for w in wrong:
+            assert not np.allclose(np.nan_to_num(w), o, rtol=1e-6, atol=1e-6), name
+
+
 # ------------------------------------------------------------ tolerances, counts, generators
 
 def test_tolerances_match_baseline_table():
