@@ -12,15 +12,21 @@ namespace sf {
 // an 8-tile LDS ring per wave where it fits (NW * 16 KB), else 4 tiles.
 template <typename TIn, typename TOut>
 static int launch_skinny_line(const GemmParams& p, const dim3& g, hipStream_t st) {
+  // x in whole 128-byte lines (a round trip through LDS) only where it has
+  // more than 8 rows: at M <= 8 the MFMA-layout loads touch as few lines.
+  const bool xline = p.M > 8;
   switch (p.K) {
     case 2048:
-      hipLaunchKernelGGL((skinny16l_kernel<TIn, TOut, 4, 8>), g, dim3(256), 0, st, p);
+      if (xline) hipLaunchKernelGGL((skinny16l_kernel<TIn, TOut, 4, 8, true>), g, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((skinny16l_kernel<TIn, TOut, 4, 8, false>), g, dim3(256), 0, st, p);
       return SF_OK;
     case 4096:
-      hipLaunchKernelGGL((skinny16l_kernel<TIn, TOut, 8, 8>), g, dim3(512), 0, st, p);
+      if (xline) hipLaunchKernelGGL((skinny16l_kernel<TIn, TOut, 8, 8, true>), g, dim3(512), 0, st, p);
+      else hipLaunchKernelGGL((skinny16l_kernel<TIn, TOut, 8, 8, false>), g, dim3(512), 0, st, p);
       return SF_OK;
     case 8192:
-      hipLaunchKernelGGL((skinny16l_kernel<TIn, TOut, 16>), g, dim3(1024), 0, st, p);
+      if (xline) hipLaunchKernelGGL((skinny16l_kernel<TIn, TOut, 16, 4, true>), g, dim3(1024), 0, st, p);
+      else hipLaunchKernelGGL((skinny16l_kernel<TIn, TOut, 16, 4, false>), g, dim3(1024), 0, st, p);
       return SF_OK;
   }
   return fail(SF_ERR_INVALID_ARG, "skinny line kernel: K=%d is not 2048, 4096 or 8192", p.K);

@@ -97,6 +97,14 @@ __device__ __forceinline__ u32x4 ds_read16(uint32_t addr) {
   return v;
 }
 
+// ds_write_b128 of a lane's 16 bytes at LDS byte address `addr` + OFF, as
+// inline assembly, so it stays in program order with the ds_read16 reads
+// (LDS runs one wave's accesses in issue order).
+template <int OFF>
+__device__ __forceinline__ void ds_write16(uint32_t addr, u32x4 v) {
+  asm volatile("ds_write_b128 %0, %1 offset:%2" : : "v"(addr), "v"(v), "i"(OFF));
+}
+
 // ds_read_b64_tr_b16 as inline assembly (as ds_read16): within each 16-lane
 // group, lane 4a + b receives element b of the 8-byte rows addressed by
 // lanes a, 4 + a, 8 + a and 12 + a (measured lane layout).

@@ -157,7 +157,7 @@ __device__ __forceinline__ void tie2(u32x4& a, u32x4& b) { asm volatile("" : "+v
 //     holds C[m = l % 16][n = 4 (l / 16) + 0..3].
 // Every wave waits only for its own loads (vmcnt) and reads only its own
 // ring, so the loop has no barrier.  Requires 16-byte aligned rows.
-template <typename TIn, typename TOut, int NW, int R = 4>
+template <typename TIn, typename TOut, int NW, int R = 4, bool XLINE = true>
 __global__ __launch_bounds__(NW * 64) void skinny16l_kernel(GemmParams p) {
   static_assert(R == 4 || R == 8, "the ring depth divides the 8 tiles of a row block");
   constexpr int TILE = 2048;  // 16 rows x 128 bytes
@@ -197,9 +197,20 @@ __global__ __launch_bounds__(NW * 64) void skinny16l_kernel(GemmParams p) {
                                              kNonTemporal);
   };
   // x fragments: slice s (k = kw + 32 s ..) lane l: row m = l & 15, 8 k at
-  // kw + 32 s + 8 (l >> 4); rows past M are zero.  Tile L of the first row
-  // block brings the two slices it needs (2 L, 2 L + 1) right after its W
-  // loads, so x (16 KB per wave at M = 16) streams beside W instead of
+  // kw + 32 s + 8 (l >> 4); rows past M are zero.  XLINE: x arrives a 64-k
+  // window (two slices) at a time in whole 128-byte row segments: load 0 of
+  // window L brings rows 0-7 (lane l: row l >> 3, chunk (l & 7) ^ (l >> 3)),
+  // load 1 rows 8-15, so each load touches 8 cache lines instead of the 16
+  // half lines that loads in the MFMA layout touch (M = 16: 16.15 -> 15.85
+  // us, measured; at M <= 8 the MFMA-layout loads touch at most 8 lines and
+  // skip the round trip through LDS: 0.06 us faster, so !XLINE there).
+  // When tile L of the first row block has been read from its ring slot,
+  // the window is written there in the W tiles' layout (lane l at slot l & 7
+  // of line l >> 3: 16 l bytes, conflict-free) and read back as two MFMA
+  // fragments with the W fragment offsets; a wave's LDS accesses run in
+  // issue order, so the W reads see the tile and the reads back see the
+  // window.  Tile L of the first row block brings its window right after
+  // its W loads, so x (16 KB per wave at M = 16) streams beside W instead of
   // holding the load path before W starts.
   // The x loads are inline assembly: the compiler would count only them
   // (not the direct loads between them) when it places its own wait before
@@ -208,16 +219,18 @@ __global__ __launch_bounds__(NW * 64) void skinny16l_kernel(GemmParams p) {
   // after that wait, so nothing reads them earlier.
   u32x4 xf[16];
   const int xm = lane & 15;
-  const uint16_t* xr = X + (int64_t)(xm < M ? xm : 0) * p.lda + kw + 8 * (lane >> 4);
+  const int xl = XLINE ? lane >> 3 : xm;
+  const int xc = XLINE ? (lane & 7) ^ xl : lane >> 4;
+  const uint16_t* xr0 = X + (int64_t)(xl < M ? xl : 0) * p.lda + kw + 8 * xc;
+  const uint16_t* xr1 = XLINE ? X + (int64_t)(xl + 8 < M ? xl + 8 : 0) * p.lda + kw + 8 * xc : xr0 + 32;
   auto xload = [&](auto Lc) {
     constexpr int L = decltype(Lc)::value;
-    xf[2 * L] = gload16_nowait<128 * L>(xr);
-    xf[2 * L + 1] = gload16_nowait<128 * L + 64>(xr);
+    xf[2 * L] = gload16_nowait<128 * L>(xr0);
+    xf[2 * L + 1] = gload16_nowait<128 * L>(xr1);
   };
   auto xtie = [&](auto Lc) {
     constexpr int L = decltype(Lc)::value;
     tie2(xf[2 * L], xf[2 * L + 1]);
-    if (xm >= M) xf[2 * L] = xf[2 * L + 1] = u32x4{0u, 0u, 0u, 0u};  // rows past M
   };
   static_for<R - 1>([&](auto Lc) {
     issue(0, Lc);
@@ -268,10 +281,20 @@ __global__ __launch_bounds__(NW * 64) void skinny16l_kernel(GemmParams p) {
         __builtin_amdgcn_sched_barrier(0);
         if (blk == 0) xtie(Lc);
         __builtin_amdgcn_sched_barrier(0);
-        const uint32_t a = ring_a + (L % R) * TILE + f0;
+        const uint32_t slot = ring_a + (L % R) * TILE;
+        const uint32_t a = slot + f0;
         const u32x4 w0 = ds_read16<0>(a);       // chunk l >> 4
         const u32x4 w1 = ds_read16<0>(a ^ 64);  // chunk 4 + (l >> 4): slot bit 2 flipped
+        if (XLINE && blk == 0) {
+          const uint32_t wa = slot + 16 * lane;
+          ds_write16<0>(wa, xf[2 * L]);
+          ds_write16<1024>(wa, xf[2 * L + 1]);
+          xf[2 * L] = ds_read16<0>(a);
+          xf[2 * L + 1] = ds_read16<0>(a ^ 64);
+        }
         __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+        __builtin_amdgcn_sched_barrier(0);
+        if (blk == 0 && xm >= M) xf[2 * L] = xf[2 * L + 1] = u32x4{0u, 0u, 0u, 0u};  // rows past M
         __builtin_amdgcn_sched_barrier(0);
         acc[blk] = Mfma16<TIn>::run(w0, xf[2 * L], acc[blk]);
         acc[blk] = Mfma16<TIn>::run(w1, xf[2 * L + 1], acc[blk]);

@@ -226,12 +226,14 @@ def test_big_nt_linear_epilogues(act):
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
 @pytest.mark.parametrize("act", [None, "silu", "gelu"])
-@pytest.mark.parametrize("mnk", [(1, 11008, 4096), (16, 4099, 2048), (9, 700, 8192)],
+@pytest.mark.parametrize("mnk", [(1, 11008, 4096), (16, 4099, 2048), (9, 700, 8192), (12, 5000, 4096),
+                                 (8, 3001, 4096)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_skinny_line_linear_epilogues(dtype, act, mnk):
     """The row-segment skinny stream (K = 512 x waves) with bias and fused
     activations: every output checked, N not a multiple of 16 or of the
-    rows per workgroup."""
+    rows per workgroup; M of 9-16 takes x in whole lines through LDS, M of
+    at most 8 in the MFMA layout."""
     m, n, k = mnk
     rng = np.random.default_rng(m * 7 + n + k)
     x = rnd(rng, (m, k), 1.0, dtype)
@@ -247,9 +249,10 @@ def test_skinny_line_linear_epilogues(dtype, act, mnk):
     check_bound(y, y64, gemm_bound(y64, absprod, k, dtype, act), "skinny line %s %s %s" % (dtype, act, mnk))
 
 
-def test_skinny_line_fp32_output():
+@pytest.mark.parametrize("m", [4, 13])
+def test_skinny_line_fp32_output(m):
     """16-bit inputs with an fp32 result through the row-segment stream."""
-    m, n, k = 4, 3000, 4096
+    n, k = 3000, 4096
     rng = np.random.default_rng(5)
     a = rnd(rng, (m, k), 1.0, "bfloat16")
     w = rnd(rng, (n, k), 1.0 / np.sqrt(k), "bfloat16")
