@@ -97,6 +97,14 @@ __device__ __forceinline__ u32x4 ds_read16(uint32_t addr) {
   return v;
 }
 
+// ds_read_b64 of 8 bytes at LDS byte address `addr` + OFF (as ds_read16).
+template <int OFF>
+__device__ __forceinline__ u32x2 ds_read8v(uint32_t addr) {
+  u32x2 v;
+  asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+
 // ds_write_b128 of a lane's 16 bytes at LDS byte address `addr` + OFF, as
 // inline assembly, so it stays in program order with the ds_read16 reads
 // (LDS runs one wave's accesses in issue order).
@@ -153,6 +161,9 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   constexpr int DMA_I = 4;                   // per operand per wave per slice pair
   __shared__ __attribute__((aligned(1024))) uint8_t sA0[OP_BYTES], sB0[OP_BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t sA1[OP_BYTES], sB1[OP_BYTES];
+  // The tile's 256 bias values, loaded with its first k-pair (two areas:
+  // the persistent kernel loads the next job's while this one's is in use).
+  __shared__ __attribute__((aligned(16))) uint16_t sBias[2][BN];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -268,6 +279,22 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
       (void*)A, (short)0, (int)(a_rows * (uint32_t)p.lda * 2u), 0x00020000);
   const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
       (void*)B, (short)0, (int)(b_rows * (uint32_t)p.ldb * 2u), 0x00020000);
+  // Bias: waves 0 and 1 each move 128 values (lane l: one dword, two
+  // values) straight into the job's bias area beside its first k-pair, so
+  // the epilogue reads them from LDS instead of waiting on global loads
+  // after the main loop (1.6 us at 4096^3, measured).  The buffer's bound is
+  // N values: columns past N read zero (their outputs are not stored).  An
+  // even N keeps every dword either inside or outside that bound; an odd N
+  // loads the bias in the epilogue as before.
+  const bool bias_lds = epi_has_bias(p.epi) && (N & 1) == 0;
+  const __amdgpu_buffer_rsrc_t rBias = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(p.bias), (short)0, (int)((uint32_t)N * 2u), 0x00020000);
+  auto bias_dma = [&](int bn0, int area) {
+    if (bias_lds && wave < 2)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rBias, (lds_ptr_t)(reinterpret_cast<uint8_t*>(&sBias[area][0]) + wave * 256),
+                                               4, (uint32_t)(bn0 + wave * 128) * 2u + (uint32_t)lane_id_fresh() * 4u, 0,
+                                               0, 0);
+  };
   // An M/N-contiguous operand needs one per-lane offset: instruction i
   // reads 64 columns (128 bytes) further, through the instruction's
   // immediate offset.  That offset also moves the LDS destination, so the
@@ -407,6 +434,7 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
       // stage whose slices (pair KP - 2) every wave has finished reading
       set_offsets(nxt.m0, nxt.n0);
       dma_at(nA, nB, nxt.t_begin * BK);
+      bias_dma(nxt.n0, (jk + 1) & 1);
     } else {
       if (!odd && t / 2 + 1 < KP) dma(nA, nB, (t + 2) * BK);
     }
@@ -429,6 +457,7 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   };
 
   dma(sA0, sB0, 0);
+  bias_dma(n0, 0);
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
   __builtin_amdgcn_s_barrier();
   for (;;) {
@@ -578,11 +607,32 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   const int act = epi_act(p.epi);
   const float alpha = p.alpha;
   float bv[FN][4];
+  if (bias_lds) {
+    // every wave passed a vmcnt(0) wait after the job's first pair (and its
+    // bias) was issued; an inline-asm read carries no wait for the next
+    // job's loads in flight
+    const uint32_t ba = lds_addr(&sBias[jk & 1][0]) + (uint32_t)(wn * WN + 4 * (elane >> 4)) * 2u;
+    u32x2 bw[FN];
+    static_for<FN>([&](auto i_c) {
+      constexpr int I = decltype(i_c)::value;
+      bw[I] = ds_read8v<I * 32>(ba);
+    });
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int i = 0; i < FN; ++i) {
+    for (int i = 0; i < FN; ++i) {
+      bv[i][0] = Elem<TIn>::to_f32(static_cast<uint16_t>(bw[i][0]));
+      bv[i][1] = Elem<TIn>::to_f32(static_cast<uint16_t>(bw[i][0] >> 16));
+      bv[i][2] = Elem<TIn>::to_f32(static_cast<uint16_t>(bw[i][1]));
+      bv[i][3] = Elem<TIn>::to_f32(static_cast<uint16_t>(bw[i][1] >> 16));
+    }
+  } else {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) bv[i][q] = 0.f;
-    if (has_bias) load_bias4<TIn>(p.bias, n0 + wn * WN + i * 16 + 4 * (elane >> 4), N, bv[i]);
+    for (int i = 0; i < FN; ++i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) bv[i][q] = 0.f;
+      if (has_bias) load_bias4<TIn>(p.bias, n0 + wn * WN + i * 16 + 4 * (elane >> 4), N, bv[i]);
+    }
   }
   constexpr int PITCH = WN * 2 + 16;             // 144 bytes
   constexpr int ROWS_S = (NSTAGE == 2 && !PERSIST) ? 64 : 32;  // 9216 / 4608 B per pass and wave

@@ -204,12 +204,14 @@ def test_tile_configs(case):
         assert np.all(np.abs(cs - cs64) <= eps * full_abs.sum(axis=0) + 1e-6), "col checksum %s" % (case,)
 
 
-@pytest.mark.parametrize("act", [None, "silu", "gelu"])
-def test_big_nt_linear_epilogues(act):
+@pytest.mark.parametrize("act,n", [(None, 8000), ("silu", 8000), ("gelu", 8000), ("silu", 7999), (None, 8191)])
+def test_big_nt_linear_epilogues(act, n):
     """The 256x256 LDS-DMA NT kernel with bias and fused activations on ragged
-    edges (M, N not tile multiples), checked on sampled rows and edge rows."""
-    m, n, k = 2100, 8000, 512
-    rng = np.random.default_rng(31)
+    edges (M, N not tile multiples), checked on sampled rows and edge rows.
+    An even N moves the tile's bias into LDS with its first k-pair; an odd N
+    loads it in the epilogue."""
+    m, k = 2100, 512
+    rng = np.random.default_rng(31 + n)
     x = rnd(rng, (m, k), 1.0, "bfloat16")
     w = rnd(rng, (n, k), 1.0 / np.sqrt(k), "bfloat16")
     b = rnd(rng, (n,), 0.5, "bfloat16")
