@@ -502,6 +502,61 @@ def pmc_summary(path: str, kernel: str | None, last: int) -> None:
             print("| %s | %.4g |" % (k, v))
 
 
+_TORCH_TIMER = r"""
+import json, sys, time
+import torch
+import torch.nn.functional as tf
+m, n, k, steps = (int(a) for a in sys.argv[1:5])
+g = torch.Generator(device="cuda").manual_seed(7)
+x = torch.randn((m, k), device="cuda", generator=g).to(torch.bfloat16)
+w = (torch.randn((n, k), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+b = (torch.randn((n,), device="cuda", generator=g) * 0.01).to(torch.bfloat16)
+res = []
+for _ in range(3):
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 0.2:  # past the power transient
+        for _ in range(10):
+            tf.linear(x, w, b)
+        torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        tf.linear(x, w, b)
+    e1.record()
+    e1.synchronize()
+    res.append(e0.elapsed_time(e1) / steps)
+print(json.dumps({"torch": torch.__version__, "ms": res}))
+"""
+
+
+def vendor_comparator(d: Dev, steps: int):
+    """Comparator only, never on the product path: the same bf16 linear
+    (x @ W^T + b) through PyTorch (torch.nn.functional.linear: hipBLASLt on
+    ROCm, in a child process with its own HIP runtime) and through this
+    library, each timed three times past the 100 ms power transient on the
+    same box.  Shapes: the north star (4096^3) and the C5 QKV projection
+    (17776 x 1920 -> 5760)."""
+    import subprocess
+    cu = d.cu
+    out = {}
+    for name, (m, n, k) in {"north_star_4096": (4096, 4096, 4096), "C5_qkv": (17776, 5760, 1920)}.items():
+        r = subprocess.run([sys.executable, "-c", _TORCH_TIMER, str(m), str(n), str(k), str(steps)],
+                           capture_output=True, text=True, timeout=600)
+        if r.returncode != 0:
+            raise RuntimeError("torch timer failed: " + r.stderr[-2000:])
+        tj = json.loads(r.stdout.strip().splitlines()[-1])
+        gx, gw, gb = d.rand((m, k), 1.0, "bfloat16"), d.rand((n, k), 0.02, "bfloat16"), d.rand((n,), 0.01, "bfloat16")
+        sf_ms = [d.time_steps(lambda i: cu.dev_linear_forward(gx, gw, gb), steps, 10) for _ in range(3)]
+        fl = 2.0 * m * n * k
+        out[name] = {"m": m, "n": n, "k": k, "torch_linear_ms": [round(v, 5) for v in tj["ms"]],
+                     "sf_linear_ms": [round(v, 5) for v in sf_ms],
+                     "torch_best_tflops": round(fl / (min(tj["ms"]) * 1e-3) / 1e12, 1),
+                     "sf_best_tflops": round(fl / (min(sf_ms) * 1e-3) / 1e12, 1), "torch": tj["torch"]}
+        log(name, out[name])
+        del gx, gw, gb
+    return {"comparator": out}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -514,6 +569,9 @@ def main(argv=None):
                     help="first run one fp32 x*1.0 pass over 1 GiB (reads 1 GiB, writes 1 GiB): the "
                          "known-traffic kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--no-headline", action="store_true")
+    ap.add_argument("--vendor-comparator", action="store_true",
+                    help="time torch.nn.functional.linear (hipBLASLt) beside this library's linear at the "
+                         "north-star and C5 QKV shapes, past the power transient, and exit (a comparator only)")
     ap.add_argument("--pmc-summary", default=None, metavar="CSV",
                     help="print a markdown summary of a rocprofv3 --pmc counter-collection CSV (the last --steps "
                          "dispatches of the kernel named by --kernel, default the most dispatched) and exit")
@@ -545,6 +603,9 @@ def main(argv=None):
         y = cu.dev_muls(src, 1.0)
         cu.device_synchronize()
         del y, src
+    if args.vendor_comparator:
+        print(json.dumps(vendor_comparator(d, args.steps)), flush=True)
+        return 0
     if args.no_headline:
         sw = sweep(d, args.steps, args.warmup, args.only)
         print(json.dumps({"sweep": sw}), flush=True)

@@ -432,6 +432,7 @@ int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
   p.ws = nullptr;
   p.counters = nullptr;
   p.persist = 0;
+  p.wave4 = 0;
   p.xcd_shift = 0;
   p.arrive_spins = kSplitArriveSpins;
   if (plan.fp32 && batch == 1 && K >= 128 && (plan.cfg == TILE32_DMA || plan.cfg == TILE32_DMA_SPLIT)) {
@@ -543,6 +544,13 @@ int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
       }
     }
     if (p.split == 0 && can_persist && 2 * R <= cus) p.persist = cus;
+    // One workgroup per tile, no split parts, deep K, C rows in whole
+    // 128-byte lines: the one-wave-per-SIMD kernel.  Measured against the
+    // 8-wave kernel on one box: 4096^3 92.4 -> 91.6 us, 4096 x 11008 x
+    // 4096 256.9 -> 255.8 us, K = 8192 175.3 -> 173.0 us; at K = 2048 and
+    // 1024 within 0.6 % either way, and 2.3 % slower with 4000-wide C rows
+    // (its 256-byte row segments straddle more lines).
+    if (a_kmajor && b_kmajor && p.split == 0 && p.persist == 0 && K >= 4096 && ldc % 64 == 0) p.wave4 = 1;
   }
   if (plan.cfg == TILE_SKINNY_LINE) {
     // One workgroup per CU where N allows, at most 64 rows of W each.
@@ -639,6 +647,8 @@ int sf_gemm_plan(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
              plan.p.tiles_m * plan.p.tiles_n - plan.p.full_tiles, plan.p.split);
   else if (!plan.noop && plan.p.persist > 0)
     snprintf(extra, sizeof(extra), " persistent");
+  else if (!plan.noop && plan.p.wave4 > 0)
+    snprintf(extra, sizeof(extra), " 4-wave");
   const char* name = plan.noop ? "noop" : tile_name(plan.cfg);
   if (!plan.noop && plan.cfg == TILE_NT_BIG)  // the LDS-DMA kernel takes every operand layout
     name = plan.a_kmajor ? (plan.b_kmajor ? "gemm nt 256x256 lds-dma" : "gemm nn 256x256 lds-dma")

@@ -84,6 +84,9 @@ struct GemmParams {
   // (kSplitArriveSpins in production).  A test sets 0 so that every part
   // but the last gives up at once and the last sums every slice.
   int arrive_spins;
+  // 256 x 256 NT kernel, one workgroup per tile and no split: 1 runs the
+  // one-wave-per-SIMD variant (gemm16nt_4w.hpp), bit-identical results.
+  int wave4;
 };
 
 // Split-tile arrival, called by one thread of a workgroup after every

@@ -3,6 +3,7 @@
 #pragma once
 
 #include "sf_internal.hpp"
+#include "gemm16nt_4w.hpp"
 #include "gemm16nt_pp.hpp"
 #include "skinny16.hpp"
 
@@ -86,6 +87,24 @@ static int launch16_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hi
       }
       if (p.K % 128 != 0 && (AKM || KM))
         return fail(SF_ERR_INVALID_ARG, "the 256x256 LDS-DMA kernel needs K %% 128 == 0 with a K-contiguous operand");
+      if constexpr (KM && AKM) {
+        if (p.wave4 > 0) {  // the planner's choice: one workgroup per tile, no split
+          if (p.split > 0 || p.K < 192)
+            return fail(SF_ERR_INVALID_ARG, "one-wave-per-SIMD 256x256 kernel: no split, K >= 192");
+          switch (epi_act(p.epi)) {
+            case ACT_SILU:
+              hipLaunchKernelGGL((gemm16nt_4w_kernel<TIn, TOut, ACT_SILU>), g, dim3(256), 0, st, p);
+              break;
+            case ACT_GELU:
+              hipLaunchKernelGGL((gemm16nt_4w_kernel<TIn, TOut, ACT_GELU>), g, dim3(256), 0, st, p);
+              break;
+            default:
+              hipLaunchKernelGGL((gemm16nt_4w_kernel<TIn, TOut, ACT_NONE>), g, dim3(256), 0, st, p);
+              break;
+          }
+          break;
+        }
+      }
       hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut, 2, AKM, KM>), g, dim3(512), 0, st, p);
       break;
     case TILE_SKINNY:

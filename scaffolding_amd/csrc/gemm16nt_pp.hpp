@@ -285,8 +285,10 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   // after the main loop (1.6 us at 4096^3, measured).  The buffer's bound is
   // N values: columns past N read zero (their outputs are not stored).  An
   // even N keeps every dword either inside or outside that bound; an odd N
-  // loads the bias in the epilogue as before.
-  const bool bias_lds = epi_has_bias(p.epi) && (N & 1) == 0;
+  // loads the bias in the epilogue as before, and so does the NN layout
+  // (dX = dY W has no bias; the persistent NN kernel has no registers to
+  // spare for the next job's bias area).
+  const bool bias_lds = B_KM && epi_has_bias(p.epi) && (N & 1) == 0;
   const __amdgpu_buffer_rsrc_t rBias = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<void*>(p.bias), (short)0, (int)((uint32_t)N * 2u), 0x00020000);
   auto bias_dma = [&](int bn0, int area) {

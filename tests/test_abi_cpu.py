@@ -154,9 +154,13 @@ def test_dispatch_for_config_shapes():
     assert plan(M=17776, N=7680, K=1920, lda=1920, ldb=1920, ldc=7680) \
         == "gemm nt 256x256 lds-dma 16-bit persistent"
     # one tile per CU (north star) and a last round more than half full
-    # (C3 M = 4096: 688 tiles) keep one workgroup per tile
-    assert plan() == "gemm nt 256x256 lds-dma 16-bit"
-    assert plan(M=4096, N=11008, ldc=11008) == "gemm nt 256x256 lds-dma 16-bit"
+    # (C3 M = 4096: 688 tiles) keep one workgroup per tile, on the
+    # one-wave-per-SIMD kernel (K >= 4096, C rows of whole 128-byte lines)
+    assert plan() == "gemm nt 256x256 lds-dma 16-bit 4-wave"
+    assert plan(M=4096, N=11008, ldc=11008) == "gemm nt 256x256 lds-dma 16-bit 4-wave"
+    assert plan(K=2048, lda=2048, ldb=2048) == "gemm nt 256x256 lds-dma 16-bit"
+    assert plan(N=4000, ldc=4000) == "gemm nt 256x256 lds-dma 16-bit"
+    assert plan(N=4000, ldc=4032) == "gemm nt 256x256 lds-dma 16-bit 4-wave"
     # whole rounds only: persistent; a split tail packs each XCD with at most
     # 32 parts (85 tail tiles: 11 on the busiest XCD, so 2 parts each)
     assert plan(N=8192, K=512, lda=512, ldb=512, ldc=8192) == "gemm nt 256x256 lds-dma 16-bit persistent"
@@ -258,7 +262,8 @@ def test_split_tail_needs_whole_tiles_per_xcd():
     host-only CU-count override (no device visible): M = 17776, N = 1920,
     K = 7680 is 560 tiles; on 248 CUs 496 whole tiles remain (persistent,
     split: at most 31 parts per XCD, 8 tail tiles on each, so 3 parts), on
-    250 CUs 500 (neither persistent nor split)."""
+    250 CUs 500 (neither persistent nor split: one workgroup per tile, on
+    the one-wave-per-SIMD kernel)."""
     code = ("import ctypes,sys;so=ctypes.CDLL(sys.argv[1]);b=ctypes.create_string_buffer(96);I=ctypes.c_int64;"
             "rc=so.sf_gemm_plan(0,1,I(17776),I(1920),I(7680),I(1),ctypes.c_void_p(256),I(7680),I(0),"
             "ctypes.c_void_p(512),I(7680),I(0),ctypes.c_void_p(1024),I(1920),I(0),2,2,ctypes.c_float(1.0),"
@@ -271,7 +276,7 @@ def test_split_tail_needs_whole_tiles_per_xcd():
         got[cus] = r.stdout.strip()
     assert got[256] == "0 gemm nt 256x256 lds-dma 16-bit persistent split-tail 48x5"
     assert got[248] == "0 gemm nt 256x256 lds-dma 16-bit persistent split-tail 64x3"
-    assert got[250] == "0 gemm nt 256x256 lds-dma 16-bit"
+    assert got[250] == "0 gemm nt 256x256 lds-dma 16-bit 4-wave"
 
 
 def test_noalloc_rejects_plans_beyond_its_scratch():
