@@ -44,7 +44,7 @@ METRIC = "GEMM TFLOP/s & % MFMA peak (bf16/fp32 linear); skinny GEMM HBM GB/s"
 PEAK_BF16 = 2.5e15      # dense bf16/fp16 MFMA, FLOP/s
 PEAK_FP32 = 157.3e12    # fp32 matrix, FLOP/s
 PEAK_HBM = 8.0e12       # HBM3E, B/s
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gemm16nt_pp_linear_4096.txt")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gemm16nt_4w_linear_4096.txt")
 SETTLE_MS = 100.0       # minimum device work in every warm-up (see Dev.time_steps)
 
 
