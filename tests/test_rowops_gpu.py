@@ -128,3 +128,20 @@ def test_bias_add(dtype):
     y64 = c.astype(np.float64) + b
     bound = out_half_ulp_rel(dtype) * np.abs(y64) + 1e-30
     assert np.all(np.abs(down(gc) - y64) <= bound)
+
+
+@pytest.mark.parametrize("n,dtype", [(40_000_001, np.float16), (16_777_219, np.float32), (1001, np.float16)],
+                         ids=["80MB-f16-ragged", "64MB-f32-ragged", "small"])
+def test_zero_fill(n, dtype):
+    """sf_zero over a block that held non-zero data: large fills (64 MB and
+    up: non-temporal stores, one workgroup per 512 16-byte stores) and a
+    small one, with sizes that leave tail bytes past the last 16-byte store.
+    The caching allocator hands the freed block back to the zero fill, so
+    every byte the fill misses would still read as one."""
+    ones = cu().gputensor_from_numpy(np.ones((n,), np.float32), -1, np.dtype(dtype))
+    del ones
+    z = cu().zeros((n,), dtype, 0)
+    cu().device_synchronize()
+    got = cu().gputensor_to_numpy(z)
+    assert got.shape == (n,)
+    assert np.count_nonzero(got) == 0
