@@ -56,6 +56,7 @@ const char* tile_name(int cfg) {
     case TILE32_SMALL2: return "gemm small 16x32";
     case TILE32_DMA: return "gemm tile 64x64 lds-dma k-groups";
     case TILE32_DMA_SPLIT: return "gemm tile 64x64 lds-dma";
+    case TILE_NT_K64: return "gemm nt 128x128 k64 lds-dma";
   }
   return "gemm";
 }
@@ -66,6 +67,7 @@ void tile_dims(int cfg, bool fp32, int& bm, int& bn) {
     case TILE_NT_BIG: bm = 256; bn = 256; return;
     case TILE_256x128: bm = 256; bn = 128; return;
     case TILE_128x128: bm = 128; bn = 128; return;
+    case TILE_NT_K64: bm = 128; bn = 128; return;
     case TILE_256x64: bm = 256; bn = 64; return;
     case TILE_SKINNY: bm = 16; bn = 32; return;
     case TILE_SKINNY_LINE: bm = 16; bn = 64; return;
@@ -141,14 +143,18 @@ static int choose_tile16(int64_t M, int64_t N, int64_t K, int64_t batch, bool ve
     return (K == 2048 || K == 4096 || K == 8192) ? TILE_SKINNY_LINE : TILE_SKINNY;
   if (f32_out) return TILE_128x128;
   auto tiles = [&](int64_t bm, int64_t bn) { return cdiv(M, bm) * cdiv(N, bn) * batch; };
-  // The LDS-DMA kernel: K-contiguous operands need K % 128 == 0 (or K == 64
-  // for NT); two M/N-contiguous operands take any K >= 128.  It runs at
-  // least half a wave of 256 x 256 tiles, or fewer for a single GEMM whose
-  // tiles the split below cuts along k.
-  const bool k_ok = (a_kmajor && b_kmajor && K == 64) || (K >= 128 && (K % 128 == 0 || (!a_kmajor && !b_kmajor)));
+  // The 256 x 256 LDS-DMA kernel: K-contiguous operands need K % 128 == 0;
+  // two M/N-contiguous operands take any K >= 128.  It runs at least half a
+  // wave of 256 x 256 tiles, or fewer for a single GEMM whose tiles the
+  // split below cuts along k.
+  const bool k_ok = K >= 128 && (K % 128 == 0 || (!a_kmajor && !b_kmajor));
   const int64_t t256 = tiles(256, 256);
   const bool fills = t256 >= cus || (!(a_kmajor && b_kmajor) && M > 64 &&
                                      (2 * t256 >= cus || (batch == 1 && K >= 1024 && 16 * t256 >= cus)));
+  // K == 64 exactly (attention scores at head size 64), NT: bound by its
+  // stores; the 128 x 128 kernel that holds four workgroups per CU, once
+  // the 128 x 128 tiles fill the CUs.
+  if (a_kmajor && b_kmajor && K == 64 && N > 64 && tiles(128, 128) >= cus) return TILE_NT_K64;
   if (k_ok && N > 64 && fills) return TILE_NT_BIG;
   if (N <= 64) return tiles(256, 64) >= cus ? TILE_256x64 : TILE_64x64;
   if (tiles(256, 256) >= cus) return TILE_256x256;
@@ -417,6 +423,8 @@ int gemm_prepare(int transA, int transB, int64_t M, int64_t N, int64_t K, int64_
     if (plan.cfg == TILE_NT_BIG && ((a_kmajor ? M : K) * lda * 2 >= (int64_t(1) << 31) ||
                                     (b_kmajor ? N : K) * ldb * 2 >= (int64_t(1) << 31)))
       plan.cfg = TILE_256x256;
+    if (plan.cfg == TILE_NT_K64 && (M * lda * 2 >= (int64_t(1) << 31) || N * ldb * 2 >= (int64_t(1) << 31)))
+      plan.cfg = TILE_128x128;
   }
   // The row-segment skinny kernel addresses 64 rows of W with 32-bit offsets.
   if (plan.cfg == TILE_SKINNY_LINE && ldb * 2 * 64 >= (int64_t(1) << 31)) plan.cfg = TILE_SKINNY;

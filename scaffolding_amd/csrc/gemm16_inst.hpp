@@ -4,6 +4,7 @@
 
 #include "sf_internal.hpp"
 #include "gemm16nt_4w.hpp"
+#include "gemm16nt_k64.hpp"
 #include "gemm16nt_pp.hpp"
 #include "skinny16.hpp"
 
@@ -59,10 +60,6 @@ static int launch16_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hi
       break;
     case TILE_NT_BIG:
       if constexpr (KM && AKM) {
-        if (p.K == 64) {
-          hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut, 1>), g, dim3(512), 0, st, p);
-          break;
-        }
         if (p.persist > 0) {
           if (p.K % 128 != 0 || p.persist % kNumXcd != 0 || gy != 1)
             return fail(SF_ERR_INVALID_ARG, "persistent 256x256 kernel: K %% 128, grid %% 8 and batch 1 required");
@@ -107,6 +104,23 @@ static int launch16_t(int cfg, const GemmParams& p, unsigned gx, unsigned gy, hi
       }
       hipLaunchKernelGGL((gemm16nt_pp_kernel<TIn, TOut, 2, AKM, KM>), g, dim3(512), 0, st, p);
       break;
+    case TILE_NT_K64:
+      if constexpr (KM && AKM) {
+        if (p.K != 64) return fail(SF_ERR_INVALID_ARG, "the K = 64 kernel got K = %d", p.K);
+        switch (epi_act(p.epi)) {
+          case ACT_SILU:
+            hipLaunchKernelGGL((gemm16nt_k64_kernel<TIn, TOut, ACT_SILU>), g, dim3(256), 0, st, p);
+            break;
+          case ACT_GELU:
+            hipLaunchKernelGGL((gemm16nt_k64_kernel<TIn, TOut, ACT_GELU>), g, dim3(256), 0, st, p);
+            break;
+          default:
+            hipLaunchKernelGGL((gemm16nt_k64_kernel<TIn, TOut, ACT_NONE>), g, dim3(256), 0, st, p);
+            break;
+        }
+        break;
+      }
+      return fail(SF_ERR_UNSUPPORTED, "the K = 64 kernel needs K-contiguous A and B");
     case TILE_SKINNY:
       if constexpr (KM && AKM) {
         // grid.x = ceil(N / 32): 2 row blocks per workgroup, K split over 4 waves.

@@ -144,17 +144,14 @@ constexpr int waitcnt_imm(int vm, int lgkm) {
   return (vm & 15) | (7 << 4) | ((lgkm & 15) << 8) | (((vm >> 4) & 3) << 14);
 }
 
-// NSTAGE = 2: the pipelined kernel above, K % 128 == 0.  NSTAGE = 1: K == 64
-// exactly (one slice pair, e.g. attention scores Q.K^T at head size 64): a
-// single 64 KB stage, so two workgroups share a CU and one's stores overlap
-// the other's loads.
+// NSTAGE = 2, the pipelined kernel above: K % 128 == 0.  (K == 64 runs
+// gemm16nt_k64_kernel, which holds four workgroups per CU.)
 template <typename TIn, typename TOut, int NSTAGE = 2, bool A_KM = true, bool B_KM = true, bool PERSIST = false,
           bool SHARED = false>
 __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
-  static_assert(NSTAGE == 1 || NSTAGE == 2, "one or two pair stages");
-  static_assert(!PERSIST || (NSTAGE == 2 && A_KM), "persistent tiles: pipelined kernel, K-contiguous A");
+  static_assert(NSTAGE == 2, "two pair stages (K == 64 runs gemm16nt_k64_kernel)");
+  static_assert(!PERSIST || A_KM, "persistent tiles: K-contiguous A");
   static_assert(!SHARED || PERSIST, "a shared split sum needs the persistent grid");
-  static_assert(NSTAGE == 2 || (A_KM && B_KM), "K == 64 stage: K-contiguous operands only");
   constexpr int BM = 256, BN = 256, BK = 32;
   constexpr int WM = 128, WN = 64, FM = WM / 16, FN = WN / 16;
   constexpr int OP_BYTES = BM * 2 * BK * 2;  // 32 KB: one operand, two slices
@@ -195,7 +192,7 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
       jb.KT = 4 * (u1 - u0);
     } else {
       jb.t_begin = 0;
-      jb.KT = NSTAGE == 2 ? 4 * KU : K / BK;
+      jb.KT = 4 * KU;
     }
   };
   // Job k of this workgroup; false when it has fewer jobs.
@@ -227,7 +224,7 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
       return true;
     } else {
       if (k > 0) return false;
-      if (NSTAGE == 2 && p.split > 0) {
+      if (p.split > 0) {
         // Every XCD gets the same share of whole tiles (a contiguous range,
         // as xcd_remap gives) followed by its share of split parts, so the
         // XCDs finish together; within an XCD the long jobs come first.
@@ -469,7 +466,7 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
     for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   if (grp == 1) __builtin_amdgcn_s_barrier();
   constexpr std::false_type no_c{};
-  if constexpr (NSTAGE == 2) {
+  {
     if (PERSIST && has_next) {
       for (int t = 0; t < KT - 4; t += 4) {
         step(t + 0, sA0, sB0, sA1, sB1, no_c);
@@ -489,9 +486,6 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
         step(t + 3, sA1, sB1, sA0, sB0, no_c);
       }
     }
-  } else {
-    step(0, sA0, sB0, sA0, sB0, no_c);  // KP == 1: no further pair is loaded
-    step(1, sA0, sB0, sA0, sB0, no_c);
   }
   if (grp == 0) __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
@@ -563,7 +557,7 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
         }
       }
     }
-  } else if (NSTAGE == 2 && part >= 0) {
+  } else if (part >= 0) {
     const int tid = wave * 64 + elane;
     float* mine = p.ws + (size_t)(split_tile * p.split + part) * (FN * FM * 512 * 4);
 #pragma unroll
@@ -637,12 +631,12 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
     }
   }
   constexpr int PITCH = WN * 2 + 16;             // 144 bytes
-  constexpr int ROWS_S = (NSTAGE == 2 && !PERSIST) ? 64 : 32;  // 9216 / 4608 B per pass and wave
+  constexpr int ROWS_S = !PERSIST ? 64 : 32;  // 9216 / 4608 B per pass and wave
   uint8_t* stage;
   if constexpr (PERSIST) {
     // stage 0 is receiving the next tile's first pair: stage 1 only
     stage = ((wave >> 2) ? sB1 : sA1) + (wave & 3) * (ROWS_S * PITCH);
-  } else if constexpr (NSTAGE == 2) {
+  } else {
     switch (wave >> 1) {
       case 0: stage = sA0; break;
       case 1: stage = sB0; break;
@@ -650,8 +644,6 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
       default: stage = sB1; break;
     }
     stage += (wave & 1) * (OP_BYTES / 2);
-  } else {
-    stage = ((wave >> 2) ? sB0 : sA0) + (wave & 3) * (ROWS_S * PITCH);
   }
   constexpr int LANES_ROW = WN * 2 / 16;
   constexpr int ROWS_I = 64 / LANES_ROW;

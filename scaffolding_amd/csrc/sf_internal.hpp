@@ -49,7 +49,9 @@ enum TileCfg {
   TILE32_SMALL1 = 9,     // 16x16 blocks, 4 waves splitting k (gemm32small.hpp)
   TILE32_SMALL2 = 10,    // 16x32 blocks, 8 waves splitting k
   TILE32_DMA = 11,       // 64x64, direct-to-LDS ring, two 4-wave k-groups (gemm32dma.hpp)
-  TILE32_DMA_SPLIT = 12  // 64x64, direct-to-LDS ring, one k-group, split-K capable
+  TILE32_DMA_SPLIT = 12,  // 64x64, direct-to-LDS ring, one k-group, split-K capable
+  // 16-bit again:
+  TILE_NT_K64 = 13  // 128x128 NT with K == 64, four workgroups per CU (gemm16nt_k64.hpp)
 };
 const char* tile_name(int cfg);
 

@@ -174,9 +174,9 @@ def test_dispatch_for_config_shapes():
     assert plan(M=16, N=11008, ldc=11008).startswith("gemm skinny line")
     # other K: the chunked stream kernel
     assert plan(M=16, N=1920, K=1920, lda=1920, ldb=1920, ldc=1920) == "gemm skinny 16-bit"
-    # C4: QK^T (K = 64) and P.V (N = 64, B N-contiguous)
+    # C4: QK^T (K = 64: the store-bound 128 x 128 kernel) and P.V (N = 64, B N-contiguous)
     assert plan(M=4096, N=4096, K=64, batch=60, lda=64, ldb=64, stride_a=4096 * 64, stride_b=4096 * 64,
-                stride_c=4096 * 4096, dtype="float16").startswith("gemm nt 256x256 lds-dma")
+                stride_c=4096 * 4096, dtype="float16") == "gemm nt 128x128 k64 lds-dma 16-bit"
     assert plan(transB=0, M=4096, N=64, K=4096, batch=60, ldb=64, ldc=64, stride_a=4096 * 4096,
                 stride_b=4096 * 64, stride_c=4096 * 64, dtype="float16").startswith("gemm tile 256x64")
     # C1 / C2 fp32: outputs of at most CUs / 4 tiles of 64 x 64 with

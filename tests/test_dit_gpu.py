@@ -135,6 +135,7 @@ RES_CASES = [  # (dtype, m, n, k, kernel name prefix)
     ("float16", 70, 200, 136, "gemm tile"),
     ("bfloat16", 300, 520, 264, "gemm tile"),
     ("bfloat16", 4096, 4096, 128, "gemm nt 256x256 lds-dma"),
+    ("float16", 2100, 4001, 64, "gemm nt 128x128 k64 lds-dma"),  # K = 64: four workgroups per CU
     ("bfloat16", 4352, 4096, 4096, "gemm nt 256x256 lds-dma 16-bit persistent split"),  # split tail
     ("float16", 4352, 7936, 256, "gemm nt 256x256 lds-dma 16-bit persistent"),  # 527 tiles, persistent
     ("float32", 70, 200, 136, "gemm small 16x16"),

@@ -131,8 +131,9 @@ TILE_CASES = [
     ("bfloat16", True, 4096, 4096, 256, 1, "gemm nt 256x256 lds-dma"),
     ("float16", True, 4000, 4100, 384, 1, "gemm nt 256x256 lds-dma"),
     ("bfloat16", True, 1000, 1100, 128, 16, "gemm nt 256x256 lds-dma"),
-    ("float16", True, 2000, 2100, 64, 8, "gemm nt 256x256 lds-dma"),
-    ("bfloat16", True, 4096, 4096, 64, 1, "gemm nt 256x256 lds-dma"),
+    ("float16", True, 2000, 2100, 64, 8, "gemm nt 128x128 k64 lds-dma"),
+    ("bfloat16", True, 4096, 4096, 64, 1, "gemm nt 128x128 k64 lds-dma"),
+    ("bfloat16", True, 1000, 4001, 64, 3, "gemm nt 128x128 k64 lds-dma"),
     ("bfloat16", False, 4096, 4096, 192, 1, "gemm tile 256x256"),
     ("float16", True, 2048, 4096, 136, 1, "gemm tile 256x128"),
     ("bfloat16", False, 2048, 4096, 136, 1, "gemm tile 256x128"),
@@ -224,6 +225,29 @@ def test_big_nt_linear_epilogues(act, n):
     y64 = ref.linear_f64(x[rows], w, b, act)
     absprod = np.abs(x[rows].astype(np.float64)) @ np.abs(w.astype(np.float64)).T
     check_bound(y[rows], y64, gemm_bound(y64, absprod, k, "bfloat16", act), "big nt %s" % act)
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("act,bias", [(None, False), (None, True), ("silu", True), ("gelu", False)])
+@pytest.mark.parametrize("mn", [(2100, 4096), (1000, 4001)], ids=lambda s: "x".join(map(str, s)))
+def test_k64_linear_epilogues(dtype, act, bias, mn):
+    """The K = 64 kernel (128 x 128 tiles, four workgroups per CU) with and
+    without bias and with fused activations, partial row and column tiles
+    and an odd N; every output against fp64."""
+    m, n = mn
+    k = 64
+    rng = np.random.default_rng(m + n + (act == "silu") + 2 * bias)
+    x = rnd(rng, (m, k), 1.0, dtype)
+    w = rnd(rng, (n, k), 1.0 / np.sqrt(k), dtype)
+    b = rnd(rng, (n,), 0.5, dtype) if bias else None
+    gx, gw = up(x, dtype), up(w, dtype)
+    plan = cu().gemm_plan(1, m, n, k, 1, gx.data_ptr, k, 0, gw.data_ptr, k, 0, n, 0, gx.dtype,
+                          epi=1 if bias else 0, ptr_bias=16 if bias else 0)
+    assert plan == "gemm nt 128x128 k64 lds-dma 16-bit", plan
+    y = down(cu().dev_linear_forward(gx, gw, up(b, dtype) if bias else None, act))
+    y64 = ref.linear_f64(x, w, b, act)
+    absprod = np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+    check_bound(y, y64, gemm_bound(y64, absprod, k, dtype, act), "k64 %s %s" % (act, bias))
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])

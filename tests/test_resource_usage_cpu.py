@@ -22,7 +22,7 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "scaffolding_amd", "csrc")
 HOT = ["gemm16_bf16.hip", "gemm16_f16.hip", "attention.hip", "gemm32.hip"]
-WATCH = re.compile(r"gemm16nt_pp_kernel|gemm16nt_4w_kernel|skinny16l_kernel|attn64_kernel|gemm32dma_kernel|gemm32small_kernel")
+WATCH = re.compile(r"gemm16nt_pp_kernel|gemm16nt_4w_kernel|gemm16nt_k64_kernel|skinny16l_kernel|attn64_kernel|gemm32dma_kernel|gemm32small_kernel")
 
 
 def _hipcc():
@@ -68,9 +68,11 @@ def test_hot_kernels_do_not_spill():
             reports = list(ex.map(lambda s: _report(s, d), HOT))
     seen = [k for r in reports for k in _kernels(r) if WATCH.search(k[0])]
     names = " ".join(k[0] for k in seen)
-    for want in ("gemm16nt_pp_kernel", "gemm16nt_4w_kernel", "skinny16l_kernel", "attn64_kernel", "gemm32dma_kernel",
+    for want in ("gemm16nt_pp_kernel", "gemm16nt_4w_kernel", "gemm16nt_k64_kernel", "skinny16l_kernel", "attn64_kernel", "gemm32dma_kernel",
                  "gemm32small_kernel"):
         assert want in names, "no %s instantiation found in the report" % want
     spilled = [k for k in seen if k[2] > 0]
     assert not spilled, "kernels using scratch (name, VGPRs, bytes/lane): %s" % spilled
     assert all(k[1] is not None and k[1] <= 256 for k in seen if "pp_kernel" in k[0] or "attn64" in k[0])
+    # four workgroups of four waves per CU
+    assert all(k[1] is not None and k[1] <= 128 for k in seen if "k64_kernel" in k[0])
