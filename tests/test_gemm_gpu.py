@@ -113,6 +113,27 @@ def test_batched(dtype, nt, bcast):
     check_bound(y, y64, gemm_bound(y64, absprod, k, dtype), "batched %s %s %s" % (dtype, nt, bcast))
 
 
+@pytest.mark.parametrize("bcast", ["b2d", "a2d"])
+def test_batched_k64_broadcast(bcast):
+    """Batched NT with K = 64 on the K = 64 kernel (128 x 128 tiles), one
+    operand broadcast over the batch (batch stride 0), alpha-scaled as the
+    attention scores are; every output against fp64."""
+    rng = np.random.default_rng(13 + (bcast == "a2d"))
+    bsz, m, n, k = 4, 1100, 1000, 64
+    a = rnd(rng, (m, k) if bcast == "a2d" else (bsz, m, k), 1.0, "float16")
+    b = rnd(rng, (n, k) if bcast == "b2d" else (bsz, n, k), 1.0, "float16")
+    ga, gb = up(a, "float16"), up(b, "float16")
+    plan = cu().gemm_plan(1, m, n, k, bsz, ga.data_ptr, k, 0 if bcast == "a2d" else m * k, gb.data_ptr, k,
+                          0 if bcast == "b2d" else n * k, n, m * n, "float16")
+    assert plan == "gemm nt 128x128 k64 lds-dma 16-bit", plan
+    y = down(cu().dev_batched_matmul_nt(ga, gb, 0.125))
+    bm = np.swapaxes(b, -2, -1)
+    y64 = 0.125 * np.matmul(a.astype(np.float64), bm.astype(np.float64))
+    absprod = 0.125 * np.matmul(np.abs(a.astype(np.float64)), np.abs(bm.astype(np.float64)))
+    assert y.shape == (bsz, m, n)
+    check_bound(y, y64, gemm_bound(y64, absprod, k, "float16"), "batched k64 %s" % bcast)
+
+
 def test_batched_nt_alpha():
     rng = np.random.default_rng(12)
     q = rnd(rng, (4, 96, 64), 1.0, "float16")
