@@ -11,18 +11,28 @@ AttnSplit attn_split_plan(const AttnShape& a, int cus) {
   sp.parts = 0;
   const int64_t nb = (a.Sk + 63) / 64;
   // Two workgroups per CU, all equally long: the items past the last whole
-  // round of slots run alone.  When that round is at most half full, its
-  // items are split into P key ranges (P * items <= slots, at least 8 key
-  // blocks a part, at most 16 parts), so the round takes about 1/P of a
-  // workgroup's time plus the combine.  Measured at 17776 tokens: 30 heads
-  // (2100 items over 512 slots) 2.47 ms unsplit against 2.13 ms for 29.
+  // round of slots (the tail) run alone.  They are split into P key ranges
+  // (at least 8 key blocks a part, at most 16 parts) when that shortens
+  // their phase: tail * P parts take ceil(tail * P / slots) rounds of
+  // nb / P key blocks each, plus about 3 key blocks' time a part for its
+  // fp32 partials and the combine, against one round of nb key blocks
+  // unsplit; the smallest such cost wins if it is under 90 % of the
+  // unsplit round.  A tail of at most half the slots takes P = slots /
+  // tail (one round).  Measured at 17776 tokens: 30 heads (2100 items over
+  // 512 slots, a tail of 52) 2.47 ms unsplit against 2.13 ms in 9 parts.
   const int64_t slots = 2 * (int64_t)cus;
   const int64_t tail = sp.items % slots;
   int64_t P = 0;
-  if (tail > 0 && 2 * tail <= slots) {
-    P = slots / tail;
-    if (P > 16) P = 16;
-    if (P > nb / 8) P = nb / 8;
+  if (tail > 0) {
+    const int64_t pmax = nb / 8 < 16 ? nb / 8 : 16;
+    double best = 0.9 * (double)nb;
+    for (int64_t q = 2; q <= pmax; ++q) {
+      const double cost = (double)((tail * q + slots - 1) / slots) * ((double)nb / (double)q + 3.0);
+      if (cost < best) {
+        best = cost;
+        P = q;
+      }
+    }
   }
   // Test hook (sf_set_test_hooks): every item split into P key ranges (at
   // most one a key block, and at most 1 GiB of partials); the results must

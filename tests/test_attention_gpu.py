@@ -215,6 +215,26 @@ def test_split_plan_on_a_short_launch(dtype):
 
 
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_split_plan_on_a_tail_past_half_the_slots(dtype):
+    """One head, 300 work items of 256 query rows, 2048 keys: on 2 x 256
+    slots the whole launch is a tail past half the slots, which the plan
+    cuts into 3 key ranges of 10-11 blocks (900 parts in two rounds of a
+    third; no test hook).  Sampled query rows of several items against
+    fp64."""
+    rng = np.random.default_rng(22)
+    sq, sk = 300 * 256, 2048
+    q = rnd(rng, (1, sq, 64), 1.0, dtype)
+    k = rnd(rng, (1, sk, 64), 1.0, dtype)
+    v = rnd(rng, (1, sk, 64), 1.0, dtype)
+    g = cu()
+    o = down(g.dev_scaled_dot_product_attention(up(q, dtype), up(k, dtype), up(v, dtype), 0.125))
+    rows = np.unique(np.r_[0, 255, 256, sq // 2, sq // 2 + 129, sq - 257, sq - 1,
+                           np.random.default_rng(3).choice(sq, 120, replace=False)])
+    ref = sdpa64(q[:, rows], k, v, 0.125)
+    assert float(np.max(np.abs(o[:, rows] - ref))) <= bound(q, k, v, 0.125, dtype)
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 @pytest.mark.parametrize("sk", [65, 100, 177, 4095])
 def test_rows_past_sk_are_never_read(dtype, sk):
     """Keys and values past Sk inside the same allocation hold NaN: the
