@@ -569,6 +569,9 @@ def main(argv=None):
                     help="first run one fp32 x*1.0 pass over 1 GiB (reads 1 GiB, writes 1 GiB): the "
                          "known-traffic kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--no-headline", action="store_true")
+    ap.add_argument("--vendor-torch-only", default=None, metavar="M,N,K",
+                    help="time only torch.nn.functional.linear at M x N x K in this process (no library "
+                         "loaded), so a profiler run on this command sees the vendor kernel (a comparator only)")
     ap.add_argument("--vendor-comparator", action="store_true",
                     help="time torch.nn.functional.linear (hipBLASLt) beside this library's linear at the "
                          "north-star and C5 QKV shapes, past the power transient, and exit (a comparator only)")
@@ -585,6 +588,11 @@ def main(argv=None):
         return 0
     if args.pmc_summary:
         pmc_summary(args.pmc_summary, args.kernel, args.steps)
+        return 0
+    if args.vendor_torch_only:
+        m, n, k = (int(v) for v in args.vendor_torch_only.split(","))
+        sys.argv = ["torch-timer", str(m), str(n), str(k), str(args.steps)]
+        exec(compile(_TORCH_TIMER, "torch-timer", "exec"), {"__name__": "__torch_timer__"})
         return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
