@@ -557,6 +557,78 @@ def vendor_comparator(d: Dev, steps: int):
     return {"comparator": out}
 
 
+# (label, stream A, stream B or -1): the stream numbers of sfp_issue
+# (scaffolding_amd/probes/hw_probes.hip)
+HW_ISSUE_CASES = [
+    ("16 x mfma16x16x32 alone", 1, -1),
+    ("8 x mfma32x32x16 alone (same flops)", 6, -1),
+    ("64 x v_fma_f32 alone", 2, -1),
+    ("32 x v_exp_f32 alone", 3, -1),
+    ("64 x (v_cvt_pk_bf16_f32 + v_xor_b32) alone", 7, -1),
+    ("64 x v_max3_f32 alone", 8, -1),
+    ("mfma16 + fma, one wave (1 : 4)", 4, -1),
+    ("mfma16 + exp, one wave (1 : 2)", 5, -1),
+    ("mfma16 | mfma16", 1, 1),
+    ("fma | fma", 2, 2),
+    ("exp | exp", 3, 3),
+    ("cvt | cvt", 7, 7),
+    ("max3 | max3", 8, 8),
+    ("fma | exp", 2, 3),
+    ("mfma16 | fma", 1, 2),
+    ("mfma16 | exp", 1, 3),
+    ("mfma16 | cvt", 1, 7),
+    ("mfma32 | fma", 6, 2),
+    ("mfma32 | exp", 6, 3),
+]
+
+
+def hw_probes() -> int:
+    """Runs the measurement kernels of libsfprobe.so (built by build.py from
+    scaffolding_amd/probes/) and prints markdown tables: cycles per
+    iteration of instruction streams alone and on a SIMD shared by two waves,
+    MFMA-only throughput on random and constant bf16 operands, and the LDS
+    read rate per CU."""
+    import ctypes
+
+    path = os.path.join(ROOT, "scaffolding_amd", "libsfprobe.so")
+    if not os.path.exists(path):
+        print("bench.py: %s is missing; run __graft_entry__.build() first" % path, file=sys.stderr)
+        return 2
+    lib = ctypes.CDLL(path)
+    dbl = ctypes.c_double
+    iters = 2000
+    print("## Issue streams (shader cycles per iteration, mean over waves; one workgroup per CU)\n")
+    print("| streams | waves per SIMD | A cycles/iter | B cycles/iter |")
+    print("|---|---|---|---|")
+    for label, a, b in HW_ISSUE_CASES:
+        cyc = (dbl * 2)()
+        rc = lib.sfp_issue(a, b, iters, cyc)
+        if rc != 0:
+            print("bench.py: sfp_issue(%d, %d) failed (%d)" % (a, b, rc), file=sys.stderr)
+            return 1
+        print("| %s | %d | %.0f | %s |" % (label, 1 if b < 0 else 2, cyc[0], "-" if b < 0 else "%.0f" % cyc[1]),
+              flush=True)
+    print("\n## MFMA only: the 4096^3 GEMM's 8.39 M v_mfma_f32_16x16x32_bf16 per launch\n")
+    print("| operands | us per launch | TFLOP/s | % of 2.5 PF |")
+    print("|---|---|---|---|")
+    for random, label in ((1, "random bf16"), (0, "constant (x = 1, w = 1/128)")):
+        us, fl = dbl(0.0), dbl(0.0)
+        rc = lib.sfp_mfma_rate(random, 2000, 300, ctypes.byref(us), ctypes.byref(fl))
+        if rc != 0:
+            print("bench.py: sfp_mfma_rate failed (%d)" % rc, file=sys.stderr)
+            return 1
+        tf = fl.value / (us.value * 1e-6) / 1e12
+        print("| %s | %.2f | %.1f | %.1f |" % (label, us.value, tf, 100 * tf * 1e12 / PEAK_BF16), flush=True)
+    bpn = dbl(0.0)
+    rc = lib.sfp_lds_read(20000, 20, ctypes.byref(bpn))
+    if rc != 0:
+        print("bench.py: sfp_lds_read failed (%d)" % rc, file=sys.stderr)
+        return 1
+    print("\n## LDS reads: ds_read_b128 only, 8 waves per CU\n")
+    print("%.1f bytes per ns per CU" % bpn.value, flush=True)
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -582,7 +654,12 @@ def main(argv=None):
     ap.add_argument("--trace-summary", default=None, metavar="CSV",
                     help="print a markdown summary of a rocprofv3 kernel-trace CSV (the last --steps "
                          "dispatches of the most launched kernel separately) and exit; no GPU use")
+    ap.add_argument("--hw-probes", action="store_true",
+                    help="run the hardware measurement kernels (libsfprobe.so: issue streams, MFMA-only rate on "
+                         "random and constant operands, LDS read rate) and exit")
     args = ap.parse_args(argv)
+    if args.hw_probes:
+        return hw_probes()
     if args.trace_summary:
         trace_summary(args.trace_summary, args.steps)
         return 0

@@ -3,7 +3,10 @@
 1. every ``csrc/*.hip`` -> object with ``hipcc --offload-arch=gfx950``
    (parallel), linked into ``scaffolding_amd/libsfgemm.so``;
 2. ``_cuda_ops.pyx`` -> C with Cython -> ``_cuda_ops*.so`` with the host C
-   compiler, linked against libsfgemm.so through an ``$ORIGIN`` rpath.
+   compiler, linked against libsfgemm.so through an ``$ORIGIN`` rpath;
+3. ``probes/*.hip`` -> ``scaffolding_amd/libsfprobe.so``: hardware
+   measurement kernels that ``bench.py --hw-probes`` runs.  No product path
+   loads it.
 
 Run ``python scaffolding_amd/build.py`` (or ``__graft_entry__.build()``).
 Artefacts stay in the source tree (git-ignored) so they travel with it.
@@ -93,9 +96,21 @@ def build_ext(verbose: bool = False) -> str:
     return target
 
 
+def build_probes(verbose: bool = False) -> str:
+    sources = sorted(glob.glob(os.path.join(PKG, "probes", "*.hip")))
+    target = os.path.join(PKG, "libsfprobe.so")
+    tmp = target + ".tmp"
+    _run([_hipcc(), *HIPCC_FLAGS, "-shared", "-o", tmp, *sources])
+    os.replace(tmp, target)
+    if verbose:
+        print("built", target, flush=True)
+    return target
+
+
 def build(verbose: bool = False) -> None:
     build_lib(verbose=verbose)
     build_ext(verbose=verbose)
+    build_probes(verbose=verbose)
 
 
 if __name__ == "__main__":
