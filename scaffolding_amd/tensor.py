@@ -186,15 +186,31 @@ def _both_gpu(a: Tensor, b: Tensor, op: str) -> None:
 
 def matmul(a: Tensor, b: Tensor) -> Tensor:
     """reference tensor.py:1480-1489: 2-D -> dev_matmul, any operand >= 3-D
-    -> dev_batched_matmul (np.matmul's batch broadcast of a 2-D operand)."""
+    -> dev_batched_matmul (np.matmul's batch broadcast of a 2-D operand).
+
+    A 1-D operand, which the reference hands to np.matmul on the host
+    (tensor.py:1494-1497), stays on the device with np.matmul's rules: a
+    vector on the left is a (1, K) row, on the right a (K, 1) column (both
+    metadata-only views), and that axis is dropped from the result."""
     _both_gpu(a, b, "matmul")
-    if a.ndim == 2 and b.ndim == 2:
-        out = _cuops.dev_matmul(a._gpu, b._gpu)
-    elif a.ndim >= 3 or b.ndim >= 3:
-        out = _cuops.dev_batched_matmul(a._gpu, b._gpu)
+    if a.ndim == 0 or b.ndim == 0:
+        raise ValueError("matmul: operands must be at least 1-D (shapes %s, %s)" % (a.shape, b.shape))
+    ga, gb = a._gpu, b._gpu
+    if a.ndim == 1:
+        ga = _cuops.dev_reshape(ga, (1, a.shape[0]))
+    if b.ndim == 1:
+        gb = _cuops.dev_reshape(gb, (b.shape[0], 1))
+    if len(ga.shape) == 2 and len(gb.shape) == 2:
+        out = _cuops.dev_matmul(ga, gb)
     else:
-        raise ValueError("matmul: 1-D operands are not on the device path (shapes %s, %s)"
-                         % (a.shape, b.shape))
+        out = _cuops.dev_batched_matmul(ga, gb)
+    if a.ndim == 1 or b.ndim == 1:
+        shape = tuple(out.shape)
+        if b.ndim == 1:
+            shape = shape[:-1]
+        if a.ndim == 1:
+            shape = shape[:-1] if b.ndim == 1 else shape[:-2] + shape[-1:]
+        out = _cuops.dev_reshape(out, shape)
     return Tensor._wrap_gpu(out, a._device)
 
 

@@ -95,11 +95,33 @@ def test_matmul_batched_broadcast(dtype, case):
         check_bound(host(y), y64, gemm_bound(y64, absprod, k, dtype), "batched %s %s" % (case, dtype))
 
 
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("case", ["vec_mat", "mat_vec", "vec_vec", "batch_vec", "vec_batch"])
+def test_matmul_1d_operands(case, dtype):
+    """1-D operands follow np.matmul (the reference's host branch,
+    tensor.py:1494-1497): a vector on the left is a row, on the right a
+    column, and that axis is dropped; the product runs on the device."""
+    rng = np.random.default_rng(["vec_mat", "mat_vec", "vec_vec", "batch_vec", "vec_batch"].index(case) * 2
+                                + (dtype == "bfloat16") + 61)
+    m, k, n = 37, 520, 70
+    shapes = {"vec_mat": ((k,), (k, n)), "mat_vec": ((m, k), (k,)), "vec_vec": ((k,), (k,)),
+              "batch_vec": ((3, m, k), (k,)), "vec_batch": ((k,), (2, k, n))}[case]
+    a = rnd(rng, shapes[0], 1.0, dtype)
+    b = rnd(rng, shapes[1], 1.0, dtype)
+    y = dev(a, dtype) @ dev(b, dtype)
+    y64 = np.matmul(a.astype(np.float64), b.astype(np.float64))
+    assert y.shape == y64.shape, (y.shape, y64.shape)
+    assert y.dtype is getattr(sf, dtype)
+    absprod = np.matmul(np.abs(a).astype(np.float64), np.abs(b).astype(np.float64))
+    got = np.asarray(host(y), dtype=np.float64)
+    check_bound(got.reshape(-1), y64.reshape(-1), gemm_bound(y64, absprod, k, dtype).reshape(-1),
+                "1-D %s %s" % (case, dtype))
+
+
 def test_matmul_refusals():
     a = dev(np.ones((4, 8), np.float32))
-    v = dev(np.ones((8,), np.float32))
-    with pytest.raises(ValueError, match="1-D"):
-        sf.matmul(a, v)
+    with pytest.raises(ValueError):
+        sf.matmul(a, dev(np.ones((7,), np.float32)))  # the vector's length is not K
     with pytest.raises(RuntimeError, match="GPU only"):
         sf.matmul(sf.Tensor(np.ones((4, 8), np.float32)), sf.Tensor(np.ones((8, 2), np.float32)))
     with pytest.raises(ValueError):
