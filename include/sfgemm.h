@@ -327,6 +327,17 @@ int sf_gelu(const void* x, void* y, int64_t n, sf_dtype dt, void* stream);
 int sf_muls(const void* x, float s, void* y, int64_t n, sf_dtype dt,
             void* stream);
 
+/* Dropout over n contiguous elements: mask[i] = 1 / (1 - p) if u_i >= p
+ * else 0, y[i] = x[i] * mask[i] (fp32 arithmetic, one rounding on store;
+ * x == y allowed; mask may be NULL).  u_i in [0, 1) comes from the
+ * counter-based Philox4x32-10 stream (seed, offset): the same arguments
+ * give the same mask on any device and launch.  0 <= p < 1.
+ * Replaces cuda_dropout_f32 (_cuda_kernels.cu:1431-1480, bound at
+ * _cuda_ops.pyx:1243-1255): the same keep rule and scale; the random
+ * stream is this library's own, not cuRAND's. */
+int sf_dropout(const void* x, void* y, void* mask, int64_t n, sf_dtype dt,
+               float p, uint64_t seed, uint64_t offset, void* stream);
+
 /* C[i,j] += bias[j] in place on a contiguous M x N matrix.
  * Replaces cuda_bias_add_row_f32 (_cuda_kernels.cu:1490-1527,
  * decl _cuda_ops_decl.h:136-137). */

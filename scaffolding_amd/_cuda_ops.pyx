@@ -26,7 +26,7 @@ Differences from the reference, on purpose:
 
 import numpy as np
 cimport numpy as cnp
-from libc.stdint cimport int64_t, uintptr_t
+from libc.stdint cimport int64_t, uint64_t, uintptr_t
 from libc.string cimport memset
 from libc.math cimport sqrt
 
@@ -105,6 +105,8 @@ cdef extern from "sfgemm.h" nogil:
     int sf_gelu(const void* x, void* y, int64_t n, sf_dtype dt, void* stream)
     int sf_muls(const void* x, float s, void* y, int64_t n, sf_dtype dt, void* stream)
     int sf_bias_add_rows(void* C, const void* bias, int64_t M, int64_t N, sf_dtype dt, void* stream)
+    int sf_dropout(const void* x, void* y, void* mask, int64_t n, sf_dtype dt, float p, uint64_t seed,
+                   uint64_t offset, void* stream)
     int sf_sum_dim(const void* x, void* out, int64_t outer, int64_t dim_size, int64_t inner,
                    sf_dtype in_dtype, sf_dtype out_dtype, void* stream)
     int sf_cast(const void* x, sf_dtype in_dtype, void* y, sf_dtype out_dtype, int64_t n, void* stream)
@@ -1109,6 +1111,46 @@ def dev_muls(gt, float scalar):
     return out
 
 
+# The random stream that dropout without an explicit seed draws from: a
+# seed (manual_seed) and an offset that every draw advances, so successive
+# calls get independent masks and a run is reproducible from its seed.
+cdef unsigned long long _rng_seed = 0
+cdef unsigned long long _rng_offset = 0
+
+
+def manual_seed(unsigned long long seed):
+    """Seeds the device random stream (dropout) and restarts its offsets.
+    The reference's cuda.manual_seed is a no-op (cuda/__init__.py:366-368)
+    and its dropout always passes seed 0 (_cuda_ops.pyx:1243)."""
+    global _rng_seed, _rng_offset
+    _rng_seed = seed
+    _rng_offset = 0
+
+
+def next_random_stream():
+    """(seed, offset) for the next draw; advances the offset."""
+    global _rng_offset
+    cdef unsigned long long o = _rng_offset
+    _rng_offset += 1
+    return _rng_seed, o
+
+
+def dev_dropout(gt, float p, unsigned long long seed=0, unsigned long long offset=0):
+    """Dropout on device (reference :1243-1255).  Returns (output, mask),
+    both in gt's dtype: mask = 1 / (1 - p) where an element is kept (with
+    probability 1 - p), else 0; output = gt * mask.  The keep decisions come
+    from the Philox4x32-10 stream (seed, offset), so equal arguments give
+    equal masks; the reference's stream is cuRAND's, so masks agree with it
+    in law, not element for element."""
+    if not (0.0 <= p < 1.0):
+        raise ValueError("dev_dropout: p must be in [0, 1), got %r" % p)
+    out = _alloc_like(gt.shape, gt.dtype, gt.device_id)
+    mask = _alloc_like(gt.shape, gt.dtype, gt.device_id)
+    _check_kernel(sf_dropout(_ptr(gt), _ptr(out), _ptr(mask), gt.numel, _sf_dtype(gt.dtype), p, seed, offset,
+                             NULL))
+    return out, mask
+
+
 def dev_softmax(gt, int dim=-1, float scale=1.0):
     """softmax(scale * x) along the last dim."""
     cdef int ndim = len(gt.shape)
@@ -1209,12 +1251,14 @@ def dev_softmax_masked(scores, mask, float scale=1.0):
     return out
 
 
-def dev_sdpa_unfused(q, k, v, scale=None, attn_mask=None):
+def dev_sdpa_unfused(q, k, v, scale=None, attn_mask=None, float dropout_p=0.0, unsigned long long seed=0,
+                     unsigned long long offset=0):
     """softmax(scale * Q K^T (+ attn_mask)) V in three launches (QK^T with
     the scale folded into its epilogue, row softmax with the additive mask
     folded in, PV), scores kept in the input dtype: the reference GPU path's
     structure (nn/functional.py:310-321), with the mask of its host branch
-    (:339-341)."""
+    (:339-341).  dropout_p > 0: dropout on the probabilities before PV
+    (:317-318), from the random stream (seed, offset) of dev_dropout."""
     d = q.shape[-1]
     s = (1.0 / sqrt(<double>d)) if scale is None else float(scale)
     scores = dev_batched_matmul_nt(q, k, s)
@@ -1223,17 +1267,21 @@ def dev_sdpa_unfused(q, k, v, scale=None, attn_mask=None):
     else:
         probs = dev_softmax_masked(scores, attn_mask)
     del scores
+    if dropout_p > 0.0:
+        probs, _ = dev_dropout(probs, dropout_p, seed, offset)
     return dev_batched_matmul(probs, v)
 
 
-def dev_scaled_dot_product_attention(q, k, v, scale=None, attn_mask=None):
+def dev_scaled_dot_product_attention(q, k, v, scale=None, attn_mask=None, float dropout_p=0.0,
+                                     unsigned long long seed=0, unsigned long long offset=0):
     """softmax(scale * Q K^T (+ attn_mask)) V  (reference GPU path
     nn/functional.py:310-321; the mask as its host branch :339-341).
     q (..., Sq, D), k and v (..., Sk, D) with equal leading dims.  One fused
     launch (sf_attention: scores never reach memory) for 16-bit inputs with
-    D a multiple of 8 up to 64, a positive finite scale and no mask;
-    otherwise, or when sf_attention declines the call
-    (SF_ERR_UNSUPPORTED), the three-launch path."""
+    D a multiple of 8 up to 64, a positive finite scale, no mask and no
+    dropout; otherwise, or when sf_attention declines the call
+    (SF_ERR_UNSUPPORTED), the three-launch path (dropout_p > 0: dev_dropout
+    on the probabilities with the stream (seed, offset))."""
     d = q.shape[-1]
     s = (1.0 / sqrt(<double>d)) if scale is None else float(scale)
     _same_dtype(q, k, 'dev_scaled_dot_product_attention')
@@ -1249,9 +1297,11 @@ def dev_scaled_dot_product_attention(q, k, v, scale=None, attn_mask=None):
     cdef int64_t batch = 1
     for e in q.shape[:-2]:
         batch *= e
-    if attn_mask is not None or q.dtype == np.float32 or d < 8 or d > 64 or d % 8 != 0 \
+    if not (0.0 <= dropout_p < 1.0):
+        raise ValueError("dev_scaled_dot_product_attention: dropout_p must be in [0, 1), got %r" % dropout_p)
+    if attn_mask is not None or dropout_p > 0.0 or q.dtype == np.float32 or d < 8 or d > 64 or d % 8 != 0 \
             or not (0.0 < s < 3.0e38):
-        return dev_sdpa_unfused(q, k, v, scale, attn_mask)
+        return dev_sdpa_unfused(q, k, v, scale, attn_mask, dropout_p, seed, offset)
     out = _alloc_like(tuple(q.shape), q.dtype, q.device_id)
     cdef int ret
     cdef void* pq = _ptr(q)

@@ -881,6 +881,17 @@ int sf_muls(const void* x, float s, void* y, int64_t n, sf_dtype dt, void* strea
   return unary_common(2, x, y, n, dt, s, stream, "sf_muls");
 }
 
+int sf_dropout(const void* x, void* y, void* mask, int64_t n, sf_dtype dt, float p, uint64_t seed,
+               uint64_t offset, void* stream) {
+  g_err[0] = 0;
+  if (!valid_dtype(dt)) return fail(SF_ERR_INVALID_ARG, "sf_dropout: unknown dtype");
+  if (n < 0) return fail(SF_ERR_INVALID_ARG, "sf_dropout: negative size");
+  if (!(p >= 0.0f && p < 1.0f)) return fail(SF_ERR_INVALID_ARG, "sf_dropout: p must be in [0, 1)");
+  if (n == 0) return SF_OK;
+  if (x == nullptr || y == nullptr) return fail(SF_ERR_INVALID_ARG, "sf_dropout: null pointer");
+  return launch_dropout(x, y, mask, n, dt, p, seed, offset, static_cast<hipStream_t>(stream));
+}
+
 int sf_bias_add_rows(void* C, const void* bias, int64_t M, int64_t N, sf_dtype dt, void* stream) {
   g_err[0] = 0;
   if (!valid_dtype(dt)) return fail(SF_ERR_INVALID_ARG, "sf_bias_add_rows: unknown dtype");

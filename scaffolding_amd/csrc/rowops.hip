@@ -226,6 +226,68 @@ __global__ __launch_bounds__(256) void unary_kernel(const void* x, void* y, int6
   }
 }
 
+// ---------------------------------------------------------------------
+// Dropout: mask[i] = scale if u_i >= p else 0, y[i] = x[i] * mask[i].
+// u_i comes from a counter-based Philox4x32-10 (Salmon, Moraes, Dror, Shaw,
+// SC 2011): key (k0, k1) = the seed's halves, counter (g, g >> 32, o0, o1)
+// for the group g = i / 4 of four elements and the 64-bit stream offset;
+// output word i % 4, top 24 bits: u_i = (r >> 8) 2^-24.  The mask depends
+// only on (seed, offset, i), never on the launch geometry.
+// ---------------------------------------------------------------------
+__device__ __forceinline__ u32x4 philox4x32_10(u32x4 c, uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    if (r) {
+      k0 += 0x9E3779B9u;
+      k1 += 0xBB67AE85u;
+    }
+    const uint32_t hi0 = __umulhi(0xD2511F53u, c[0]), lo0 = 0xD2511F53u * c[0];
+    const uint32_t hi1 = __umulhi(0xCD9E8D57u, c[2]), lo1 = 0xCD9E8D57u * c[2];
+    c = u32x4{hi1 ^ c[1] ^ k0, lo1, hi0 ^ c[3] ^ k1, lo0};
+  }
+  return c;
+}
+
+// Each thread takes 8 elements (two Philox groups) per step.
+template <typename T>
+__global__ __launch_bounds__(256) void dropout_kernel(const void* x, void* y, void* mask, int64_t n, float p,
+                                                      float scale, uint32_t k0, uint32_t k1, uint32_t o0,
+                                                      uint32_t o1, bool vec) {
+  const int64_t stride = (int64_t)gridDim.x * 256 * 8;
+  for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8; i < n; i += stride) {
+    float v[8], m[8];
+    const bool full = vec && i + 8 <= n;
+    if (full) {
+      Chunk8<T>::load(x, i, v);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (i + e < n) ? Chunk8<T>::get(x, i + e) : 0.f;
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint64_t g = (uint64_t)(i >> 2) + h;
+      const u32x4 r = philox4x32_10(u32x4{(uint32_t)g, (uint32_t)(g >> 32), o0, o1}, k0, k1);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float u = (float)(r[q] >> 8) * (1.0f / 16777216.0f);
+        m[4 * h + q] = u >= p ? scale : 0.f;
+        v[4 * h + q] *= m[4 * h + q];
+      }
+    }
+    if (full) {
+      Chunk8<T>::store(y, i, v);
+      if (mask != nullptr) Chunk8<T>::store(mask, i, m);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (i + e < n) {
+          Chunk8<T>::put(y, i + e, v[e]);
+          if (mask != nullptr) Chunk8<T>::put(mask, i + e, m[e]);
+        }
+    }
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void bias_rows_kernel(void* C, const void* bias, int64_t M,
                                                         int64_t N) {
@@ -523,6 +585,24 @@ int launch_unary(int op, const void* x, void* y, int64_t n, sf_dtype dt, float s
   else if (dt == SF_F16) unary_launch_t<F16>(op, x, y, n, s, st);
   else unary_launch_t<BF16>(op, x, y, n, s, st);
   return check_launch("elementwise");
+}
+
+template <typename T>
+static void dropout_launch_t(const void* x, void* y, void* mask, int64_t n, float p, float scale, uint64_t seed,
+                             uint64_t offset, hipStream_t st) {
+  const bool vec = aligned16(x) && aligned16(y) && (mask == nullptr || aligned16(mask));
+  const unsigned grid = grid_for((n + 7) / 8);
+  hipLaunchKernelGGL((dropout_kernel<T>), dim3(grid), dim3(256), 0, st, x, y, mask, n, p, scale, (uint32_t)seed,
+                     (uint32_t)(seed >> 32), (uint32_t)offset, (uint32_t)(offset >> 32), vec);
+}
+
+int launch_dropout(const void* x, void* y, void* mask, int64_t n, sf_dtype dt, float p, uint64_t seed,
+                   uint64_t offset, hipStream_t st) {
+  const float scale = 1.0f / (1.0f - p);
+  if (dt == SF_F32) dropout_launch_t<float>(x, y, mask, n, p, scale, seed, offset, st);
+  else if (dt == SF_F16) dropout_launch_t<F16>(x, y, mask, n, p, scale, seed, offset, st);
+  else dropout_launch_t<BF16>(x, y, mask, n, p, scale, seed, offset, st);
+  return check_launch("dropout");
 }
 
 int launch_bias_rows(void* C, const void* bias, int64_t M, int64_t N, sf_dtype dt, hipStream_t st) {

@@ -144,6 +144,8 @@ struct MaskArgs {
 int launch_softmax_masked(const void* x, void* y, int64_t rows, int64_t cols, sf_dtype dt, float scale,
                           const MaskArgs& ma, sf_dtype mask_dt, hipStream_t st);
 int launch_unary(int op, const void* x, void* y, int64_t n, sf_dtype dt, float s, hipStream_t st);
+int launch_dropout(const void* x, void* y, void* mask, int64_t n, sf_dtype dt, float p, uint64_t seed,
+                   uint64_t offset, hipStream_t st);
 int launch_bias_rows(void* C, const void* bias, int64_t M, int64_t N, sf_dtype dt, hipStream_t st);
 int launch_cast(const void* x, sf_dtype in, void* y, sf_dtype out, int64_t n, hipStream_t st);
 int launch_zero(void* p, size_t nbytes, hipStream_t st);

@@ -5,6 +5,18 @@ from __future__ import annotations
 from .. import _cuda_ops as _cuops
 
 
+def manual_seed(seed: int) -> None:
+    """Seeds the device random stream that dropout draws from (reference
+    cuda/__init__.py:366-368, a no-op there)."""
+    _cuops.manual_seed(int(seed))
+
+
+def manual_seed_all(seed: int) -> None:
+    """One random stream serves every device (reference
+    cuda/__init__.py:371-373)."""
+    _cuops.manual_seed(int(seed))
+
+
 def is_available() -> bool:
     return _cuops.get_device_count() > 0
 

@@ -213,8 +213,8 @@ class Sequential(Module):
 
 
 class Dropout(Module):
-    """Identity in eval mode or at p = 0 (reference nn/layers.py:339-353);
-    random dropout is not on the device path."""
+    """Identity in eval mode or at p = 0; in training, F.dropout (reference
+    nn/layers.py:339-353)."""
 
     def __init__(self, p: float = 0.5):
         super().__init__()
@@ -223,7 +223,8 @@ class Dropout(Module):
     def forward(self, x: Tensor) -> Tensor:
         if not self.training or self.p == 0.0:
             return x
-        raise NotImplementedError("Dropout with p > 0 in training mode is not on the device path")
+        from . import functional as F
+        return F.dropout(x, self.p, True)
 
 
 class LayerNorm(Module):

@@ -116,6 +116,15 @@ def test_rowops_validation(lib):
     assert lib.sf_sum_dim(None, None, I64(0), I64(4), I64(3), 0, 0, None) == 0
     assert lib.sf_sum_dim(None, None, I64(1), I64(-1), I64(3), 0, 0, None) == -2
     assert lib.sf_sum_dim(None, None, I64(1), I64(4), I64(3), 2, 1, None) == -3
+    U64 = ctypes.c_uint64
+    drop = lambda n, p, dt=0: lib.sf_dropout(None, None, None, I64(n), dt, ctypes.c_float(p), U64(0), U64(0), None)
+    assert drop(4, 0.5) == -2                    # null pointers
+    assert drop(4, 1.0) == -2 and b"p must be" in lib.sf_last_error()
+    assert drop(4, -0.1) == -2
+    assert drop(4, float("nan")) == -2
+    assert drop(-1, 0.5) == -2
+    assert drop(4, 0.5, dt=7) == -2              # unknown dtype
+    assert drop(0, 0.5) == 0                     # empty: nothing to do
 
 
 def plan(**kw):

@@ -215,8 +215,8 @@ def test_sdpa_refusals_and_explicit_scale():
     tq = dev(q, "bfloat16")
     with pytest.raises(ValueError, match="broadcast"):  # a (2, 40, 64) mask on (2, 40, 40) scores
         F.scaled_dot_product_attention(tq, tq, tq, attn_mask=tq)
-    with pytest.raises(NotImplementedError):
-        F.scaled_dot_product_attention(tq, tq, tq, dropout_p=0.1)
+    with pytest.raises(ValueError, match="dropout_p"):
+        F.scaled_dot_product_attention(tq, tq, tq, dropout_p=1.0)
     with pytest.raises(RuntimeError, match="GPU only"):
         F.scaled_dot_product_attention(sf.Tensor(q), sf.Tensor(q), sf.Tensor(q))
     o = F.scaled_dot_product_attention(tq, tq, tq, scale=0.3)

@@ -117,8 +117,9 @@ def test_masked_sdpa_golden_fixture(name):
 
 
 def test_masked_sdpa_refusals():
-    """A mask that does not broadcast, or dropout, is refused before any
-    launch; a fully masked row gives NaN, as the reference's NumPy does."""
+    """A mask that does not broadcast, or a dropout_p outside [0, 1), is
+    refused before any launch; a fully masked row gives NaN, as the
+    reference's NumPy does."""
     from scaffolding_amd.nn import functional as F
     import scaffolding_amd as sf
     g = cu()
@@ -129,8 +130,8 @@ def test_masked_sdpa_refusals():
         g.dev_scaled_dot_product_attention(gq, gq, gq, None, up(np.zeros((3, 16, 16), np.float32), "float32"))
     dev = sf.device("cuda:0")
     tq = sf.Tensor(q, device=dev)
-    with pytest.raises(NotImplementedError, match="dropout"):
-        F.scaled_dot_product_attention(tq, tq, tq, dropout_p=0.1)
+    with pytest.raises(ValueError, match="dropout_p"):
+        F.scaled_dot_product_attention(tq, tq, tq, dropout_p=-0.1)
     mask = np.zeros((16, 16), np.float32)
     mask[3, :] = -np.inf
     o = down(g.dev_scaled_dot_product_attention(gq, gq, gq, None, up(mask, "float32")))
