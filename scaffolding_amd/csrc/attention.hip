@@ -77,10 +77,17 @@ int launch_attention(const AttnShape& a, float scale, sf_dtype dt, const AttnSpl
   for (int64_t i0 = 0; i0 < wgs; i0 += kChunk) {
     const int64_t n = (wgs - i0) < kChunk ? (wgs - i0) : kChunk;
     p.item0 = i0;
-    if (dt == SF_F16)
-      hipLaunchKernelGGL((attn64_kernel<F16>), dim3((unsigned)n), dim3(256), 0, st, p);
-    else
-      hipLaunchKernelGGL((attn64_kernel<BF16>), dim3((unsigned)n), dim3(256), 0, st, p);
+    // Q pre-scaled by scale log2 e (attn64_kernel's PRESCALE) for fp16 where
+    // that cannot overflow the format; bf16 keeps the FMA (its 8-bit
+    // significand would add a rounding of about |x| 2^-9 to every exponent).
+    if (dt == SF_F16) {
+      if (p.scale_log2e <= 1.0f)
+        hipLaunchKernelGGL((attn64_kernel<F16, true>), dim3((unsigned)n), dim3(256), 0, st, p);
+      else
+        hipLaunchKernelGGL((attn64_kernel<F16, false>), dim3((unsigned)n), dim3(256), 0, st, p);
+    } else {
+      hipLaunchKernelGGL((attn64_kernel<BF16, false>), dim3((unsigned)n), dim3(256), 0, st, p);
+    }
     const int rc = check_launch("attention");
     if (rc != SF_OK) return rc;
   }

@@ -13,11 +13,14 @@
 //      read from LDS (ds_read_b128, 128-byte lines, chunk h at slot
 //      h ^ (row & 7), conflict-free as in the GEMM kernels);
 //   2. keeps the softmax in the exp2 domain against a per-row reference m
-//      that is raised lazily: the exponents x = S scale log2 e - m are formed
-//      in place, and only when one exceeds 8 does the wave reduce the row
-//      maxima across the four lanes sharing a row, raise m and scale O and
-//      the row sums by 2^(m_old - m_new), so P = 2^x stays <= 2^8 and the
-//      common path needs no cross-lane traffic;
+//      that is raised lazily: the exponents x = S scale log2 e - m come
+//      straight out of the score MFMAs (PRESCALE: Q is multiplied by
+//      scale log2 e once per work item, rounded once into T, and each score
+//      chain starts from -m as its C operand; otherwise one FMA per score
+//      forms x in place), and only when one exceeds 8 does the wave reduce
+//      the row maxima across the four lanes sharing a row, raise m and
+//      scale O and the row sums by 2^(m_old - m_new), so P = 2^x stays
+//      <= 2^8 and the common path needs no cross-lane traffic;
 //   3. packs P to 16 bits (v_cvt_pk) and adds P V into the 64 x 64 fp32 O
 //      accumulator (32 MFMAs, V fragments from ds_read_b64_tr_b16, gfx950's
 //      transposing LDS read) and P 1 into the row sums (8 MFMAs against a
@@ -127,7 +130,13 @@ __device__ __forceinline__ void attn_store_rows(const AttnParams& p, uint16_t* O
   }
 }
 
-template <typename T>
+// PRESCALE: Q is scaled by scale log2 e in registers (the host takes it for
+// bf16, whose range holds any product, and for fp16 when scale log2 e <= 1,
+// so |Q scale log2 e| <= |Q| cannot overflow).  It removes the 64 FMAs per
+// key block and wave that form the exponents, at the cost of one extra
+// rounding of each Q element into T (bf16: relative 2^-9, below the
+// rounding of P itself).
+template <typename T, bool PRESCALE>
 __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
   constexpr int NS = 3;
   constexpr int KB = 64;
@@ -195,6 +204,20 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
     }
   }
 
+  const float sc = p.scale_log2e;
+  if constexpr (PRESCALE) {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t w = qf[mb][kc][e];
+          qf[mb][kc][e] = pack2<T>(Elem<T>::to_f32((uint16_t)(w & 0xffffu)) * sc,
+                                   Elem<T>::to_f32((uint16_t)(w >> 16)) * sc);
+        }
+  }
+
   f32x4 o[4][4], osum[4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
@@ -202,10 +225,11 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
 #pragma unroll
     for (int db = 0; db < 4; ++db) o[mb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  float mrow[4];
+  // -m per row block, all four values equal: the score MFMAs' C operand
+  // (PRESCALE) and the FMAs' addend otherwise; set by the first key block
+  f32x4 nq[4];
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) mrow[mb] = 0.f;  // set by the first key block
-  const float sc = p.scale_log2e;
+  for (int mb = 0; mb < 4; ++mb) nq[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
   // 16-bit 1.0 in both halves of every dword: the X fragment of a ones block.
   const uint32_t one2 = (uint32_t)Elem<T>::from_f32(1.0f) * 0x10001u;
   const u32x4 ones = u32x4{one2, one2, one2, one2};
@@ -246,7 +270,8 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
       __builtin_amdgcn_sched_barrier(0);
       // Independent chains back to back: all kc = 0 products, then kc = 1.
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) s[mb][NBK] = Mfma16<T>::run(kf0, qf[mb][0], f32x4{0.f, 0.f, 0.f, 0.f});
+      for (int mb = 0; mb < 4; ++mb)
+        s[mb][NBK] = Mfma16<T>::run(kf0, qf[mb][0], PRESCALE ? nq[mb] : f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) s[mb][NBK] = Mfma16<T>::run(kf1, qf[mb][1], s[mb][NBK]);
       __builtin_amdgcn_sched_barrier(0);
@@ -287,15 +312,15 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
     }
 
     // ---- online softmax with lazy rescale --------------------------------
-    // x = s scale log2(e) - m in place (the exponent of P, one FMA per score);
-    // each lane checks its 16 values of each row against THRESH.  Only when
+    // x = s scale log2(e) - m (the exponent of P: the score MFMAs' result
+    // with PRESCALE, else one FMA per score in place); each lane checks its
+    // 16 values of each row against THRESH.  Only when
     // some value exceeds it, and always in the first key block (which sets m
     // from m = 0, with O and the sums still zero), does the wave reduce the
     // row maxima across the four lanes of each row, raise m by dm, lower x
     // by dm and scale O and the row sums by 2^-dm (the first key block of
     // a split part likewise sets its own m).  Otherwise P = 2^x <=
-    // 2^THRESH.  The maxima run on FMA results, which need no quieting of
-    // signalling NaNs (the MFMA outputs would), against a constant.
+    // 2^THRESH.
     //
     // fp16 (PCHECK): after the first key block the check runs on the packed
     // P instead, three values per v_pk_maximum3_f16 (4 instructions per row
@@ -322,7 +347,8 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
       // the first block sets m to the row maximum (finite: every row has a
       // valid key there); later blocks only raise it
       const float dm = first ? mx : fmaxf(mx, 0.f);
-      mrow[mb] += dm;
+      const float nm = nq[mb][0] - dm;
+      nq[mb] = f32x4{nm, nm, nm, nm};
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
@@ -338,11 +364,12 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
     float lmx[4];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
-      const float nm = -mrow[mb];
+      if constexpr (!PRESCALE) {
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
+        for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) s[mb][nb][q] = __builtin_fmaf(s[mb][nb][q], sc, nm);
+          for (int q = 0; q < 4; ++q) s[mb][nb][q] = __builtin_fmaf(s[mb][nb][q], sc, nq[mb][0]);
+      }
       if (!PCHECK || first) {
         lmx[mb] = row_max(mb);
         need |= lmx[mb] > THRESH;
@@ -452,7 +479,7 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
     for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
       for (int db = 0; db < 4; ++db) po[(mb * 4 + db) * 64] = o[mb][db];
-      pml[mb * 64] = float2{mrow[mb], osum[mb][0]};
+      pml[mb * 64] = float2{-nq[mb][0], osum[mb][0]};
     }
     return;
   }

@@ -89,6 +89,29 @@ def test_fused_attention_large_scores_and_leading_dims():
     assert float(np.max(np.abs(o - o64))) <= bound(q, k, v, 1.0, "float16")
 
 
+@pytest.mark.parametrize("dtype,scale,qmul,kmul", [
+    ("float16", 0.6, 1.0, 1.0),     # scale log2 e = 0.87: Q pre-scaled in registers
+    ("float16", 0.125, 3.0, 3.0),   # pre-scaled, scores of magnitude ~50 from larger inputs
+    ("bfloat16", 1.0, 1.0, 1.0),    # bf16: the FMA path
+    ("float16", 2.0, 1e4, 1e-4),    # scale log2 e = 2.9: |Q| up to ~4e4 would overflow fp16 if pre-scaled
+], ids=["f16-prescaled", "f16-prescaled-large", "bf16-fma-path", "f16-fma-path"])
+def test_prescaled_and_fma_exponent_paths(dtype, scale, qmul, kmul):
+    """The two ways the kernel forms x = s scale log2 e - m (Q pre-scaled
+    with -m as the score MFMAs' C operand, or one FMA per score), with large
+    scores that need the running-maximum raise (a late key dominates)."""
+    rng = np.random.default_rng(int(scale * 10) + (dtype == "bfloat16"))
+    q = quantize((rng.standard_normal((2, 200, 64)) * qmul).astype(np.float32), dtype)
+    k = rng.standard_normal((2, 320, 64)).astype(np.float32)
+    k[:, 290] = q[:, 0:1].mean(axis=1) / qmul * 4  # one late key dominates some rows
+    k = quantize(k * kmul, dtype)
+    v = rnd(rng, (2, 320, 64), 1.0, dtype)
+    g = cu()
+    o = down(g.dev_scaled_dot_product_attention(up(q, dtype), up(k, dtype), up(v, dtype), scale))
+    o64 = sdpa64(q, k, v, scale)
+    assert np.all(np.isfinite(o))
+    assert float(np.max(np.abs(o - o64))) <= bound(q, k, v, scale, dtype)
+
+
 @pytest.mark.parametrize("shape", [(2, 40, 100, 64), (1, 64, 64, 32), (1, 33, 128, 80)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_other_shapes(shape):
