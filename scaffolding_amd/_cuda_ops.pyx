@@ -1135,19 +1135,20 @@ def next_random_stream():
     return _rng_seed, o
 
 
-def dev_dropout(gt, float p, unsigned long long seed=0, unsigned long long offset=0):
+def dev_dropout(gt, float p, unsigned long long seed=0, unsigned long long offset=0, bint with_mask=True):
     """Dropout on device (reference :1243-1255).  Returns (output, mask),
     both in gt's dtype: mask = 1 / (1 - p) where an element is kept (with
     probability 1 - p), else 0; output = gt * mask.  The keep decisions come
     from the Philox4x32-10 stream (seed, offset), so equal arguments give
     equal masks; the reference's stream is cuRAND's, so masks agree with it
-    in law, not element for element."""
+    in law, not element for element.  with_mask=False neither allocates nor
+    writes the mask and returns (output, None)."""
     if not (0.0 <= p < 1.0):
         raise ValueError("dev_dropout: p must be in [0, 1), got %r" % p)
     out = _alloc_like(gt.shape, gt.dtype, gt.device_id)
-    mask = _alloc_like(gt.shape, gt.dtype, gt.device_id)
-    _check_kernel(sf_dropout(_ptr(gt), _ptr(out), _ptr(mask), gt.numel, _sf_dtype(gt.dtype), p, seed, offset,
-                             NULL))
+    mask = _alloc_like(gt.shape, gt.dtype, gt.device_id) if with_mask else None
+    cdef void* pm = _ptr(mask) if with_mask else NULL
+    _check_kernel(sf_dropout(_ptr(gt), _ptr(out), pm, gt.numel, _sf_dtype(gt.dtype), p, seed, offset, NULL))
     return out, mask
 
 
@@ -1268,7 +1269,7 @@ def dev_sdpa_unfused(q, k, v, scale=None, attn_mask=None, float dropout_p=0.0, u
         probs = dev_softmax_masked(scores, attn_mask)
     del scores
     if dropout_p > 0.0:
-        probs, _ = dev_dropout(probs, dropout_p, seed, offset)
+        probs, _ = dev_dropout(probs, dropout_p, seed, offset, False)
     return dev_batched_matmul(probs, v)
 
 

@@ -55,7 +55,7 @@ def dropout(input: Tensor, p: float = 0.5, training: bool = True) -> Tensor:
     if input._gpu is None:
         _gpu_only("dropout")
     seed, offset = _cuops.next_random_stream()
-    out, _ = _cuops.dev_dropout(input._gpu, p, seed, offset)
+    out, _ = _cuops.dev_dropout(input._gpu, p, seed, offset, False)
     return Tensor._wrap_gpu(out, input._device)
 
 

@@ -58,6 +58,8 @@ def test_streams_and_edge_cases():
     assert np.array_equal(a, down(g.dev_dropout(x, 0.5, 5, 0)[1]))  # same stream, same mask
     assert not np.array_equal(a, down(g.dev_dropout(x, 0.5, 5, 1)[1]))  # next offset
     assert not np.array_equal(a, down(g.dev_dropout(x, 0.5, 6, 0)[1]))  # other seed
+    y1, m1 = g.dev_dropout(x, 0.5, 5, 0, False)  # no mask: the same output
+    assert m1 is None and np.array_equal(down(y1), down(x) * a)
     y0, m0 = g.dev_dropout(x, 0.0, 5)
     assert np.array_equal(down(y0), down(x)) and np.all(down(m0) == 1.0)
     with pytest.raises(ValueError):
