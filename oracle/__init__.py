@@ -22,5 +22,5 @@ Pinning (each function's checks live in tests/test_oracle.py):
     silu(x) = x/2 (1 + tanh(x/2)) and gelu(x) - gelu(-x) = x;
   * softmax / sdpa: rows sum to 1, shift invariance, a known answer
     softmax([0, ln 2]) = [1/3, 2/3], uniform weights for equal scores;
-  * tolerances: the figures BASELINE.md tabulates.
+  * tolerances: BASELINE.json's north_star formulas at tabulated sizes.
 """

@@ -4,8 +4,9 @@ Each oracle function meets at least one check that a plausible mistake (a
 dropped term, a wrong sign or index, a transposed operand) fails:
 IEEE known answers for the quantizers, brute-force fsum fixtures for the
 GEMM / linear restatements, closed-form identities for the activations,
-invariants and a known answer for softmax / SDPA, BASELINE.md's tabulated
-figures for the tolerances and work counts, and SHA-256 fingerprints for
+invariants and a known answer for softmax / SDPA, the tolerance formulas
+of BASELINE.json's north_star evaluated at tabulated sizes and the work
+counts, and SHA-256 fingerprints for
 the seeded config generators."""
 from __future__ import annotations
 
