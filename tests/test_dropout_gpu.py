@@ -104,7 +104,7 @@ def test_functional_and_module_dropout():
     assert layer(t) is t
 
 
-@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
 def test_sdpa_dropout_against_oracle(dtype):
     """softmax(scale q k^T) -> dropout (the stream after manual_seed, first
     draw) -> @ v, the reference GPU branch's order (nn/functional.py:314-321),
@@ -128,8 +128,9 @@ def test_sdpa_dropout_against_oracle(dtype):
         assert err <= 50 * tol_fp32(s) * (1 + float(np.max(np.abs(o64)))), err
     else:
         # scores, probabilities and the dropped probabilities each round
-        # into bf16 before PV: a few bf16 ulps of the output's scale
-        assert err <= tol_16(s) + 4 * 2.0 ** -8 * float(np.max(np.abs(v))) / (1 - p), err
+        # into the dtype before PV: a few ulps of the output's scale
+        eps = 2.0 ** -8 if dtype == "bfloat16" else 2.0 ** -11
+        assert err <= tol_16(s) + 4 * eps * float(np.max(np.abs(v))) / (1 - p), err
     # without dropout the same call takes the fused or unfused path unchanged
     o0 = np.asarray(F.scaled_dot_product_attention(tq, tk, tv).numpy(), np.float64)
     assert float(np.max(np.abs(o0 - ref.sdpa_f64(q, k, v, scale)))) <= tol_16(s) + 2.0 ** -7
