@@ -214,10 +214,10 @@ int sf_sum_dim(const void* x, void* out, int64_t outer, int64_t dim_size, int64_
  * Q[b] Sq x D, K[b] and V[b] Sk x D, O[b] Sq x D, row strides ld*,
  * batch strides stride* (elements), 16-bit dtype (F16 or BF16), fp32
  * accumulation and softmax.  One launch; the Sq x Sk scores never reach
- * memory.  F16 with scale * log2(e) <= 1 multiplies Q by scale * log2(e)
- * in registers (one more rounding of each Q element into fp16) so the
- * score products come out as exponents; otherwise the scale is applied
- * to the fp32 scores.  Replaces the three-launch GPU path of
+ * memory.  With scale * log2(e) <= 1 (the usual 1/sqrt(D)) Q is
+ * multiplied by scale * log2(e) in registers, one more rounding of each Q
+ * element into the dtype, so the score products come out as exponents;
+ * otherwise the scale is applied to the fp32 scores.  Replaces the three-launch GPU path of
  * scaled_dot_product_attention (nn/functional.py:310-321: dev_batched_matmul_nt,
  * dev_muls, dev_softmax, dev_batched_matmul) when there is no mask and no
  * dropout.  Requires D a multiple of 8 up to 64 (other head sizes return

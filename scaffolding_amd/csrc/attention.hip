@@ -77,16 +77,22 @@ int launch_attention(const AttnShape& a, float scale, sf_dtype dt, const AttnSpl
   for (int64_t i0 = 0; i0 < wgs; i0 += kChunk) {
     const int64_t n = (wgs - i0) < kChunk ? (wgs - i0) : kChunk;
     p.item0 = i0;
-    // Q pre-scaled by scale log2 e (attn64_kernel's PRESCALE) for fp16 where
-    // that cannot overflow the format; bf16 keeps the FMA (its 8-bit
-    // significand would add a rounding of about |x| 2^-9 to every exponent).
+    // Q pre-scaled by scale log2 e (attn64_kernel's PRESCALE) when
+    // scale log2 e <= 1: the usual 1/sqrt(D) scales (D >= 3), where it
+    // cannot overflow fp16 and Q's extra rounding moves each exponent by
+    // about 2^-9 (bf16) or 2^-12 (fp16) of the logit's size; larger scales
+    // keep the FMA on the fp32 scores.
+    const bool pre = p.scale_log2e <= 1.0f;
     if (dt == SF_F16) {
-      if (p.scale_log2e <= 1.0f)
+      if (pre)
         hipLaunchKernelGGL((attn64_kernel<F16, true>), dim3((unsigned)n), dim3(256), 0, st, p);
       else
         hipLaunchKernelGGL((attn64_kernel<F16, false>), dim3((unsigned)n), dim3(256), 0, st, p);
     } else {
-      hipLaunchKernelGGL((attn64_kernel<BF16, false>), dim3((unsigned)n), dim3(256), 0, st, p);
+      if (pre)
+        hipLaunchKernelGGL((attn64_kernel<BF16, true>), dim3((unsigned)n), dim3(256), 0, st, p);
+      else
+        hipLaunchKernelGGL((attn64_kernel<BF16, false>), dim3((unsigned)n), dim3(256), 0, st, p);
     }
     const int rc = check_launch("attention");
     if (rc != SF_OK) return rc;

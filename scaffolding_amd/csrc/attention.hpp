@@ -130,12 +130,13 @@ __device__ __forceinline__ void attn_store_rows(const AttnParams& p, uint16_t* O
   }
 }
 
-// PRESCALE: Q is scaled by scale log2 e in registers (the host takes it for
-// bf16, whose range holds any product, and for fp16 when scale log2 e <= 1,
-// so |Q scale log2 e| <= |Q| cannot overflow).  It removes the 64 FMAs per
-// key block and wave that form the exponents, at the cost of one extra
-// rounding of each Q element into T (bf16: relative 2^-9, below the
-// rounding of P itself).
+// PRESCALE: Q is scaled by scale log2 e in registers (the host takes it
+// when scale log2 e <= 1, so |Q scale log2 e| <= |Q| cannot overflow
+// fp16).  It removes the 64 FMAs per key block and wave that form the
+// exponents, at the cost of one extra rounding of each Q element into T:
+// each exponent moves by about 2^-9 (bf16) or 2^-12 (fp16) of the size of
+// the products q_d k_d, below P's own rounding for logits of a few units
+// and a few times the FMA path's error for logits of tens.
 template <typename T, bool PRESCALE>
 __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
   constexpr int NS = 3;

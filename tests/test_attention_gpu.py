@@ -5,6 +5,7 @@ dims, both 16-bit dtypes, the fallback shapes and the ABI's refusals."""
 from __future__ import annotations
 
 import ctypes
+import math
 import os
 
 import numpy as np
@@ -92,13 +93,19 @@ def test_fused_attention_large_scores_and_leading_dims():
 @pytest.mark.parametrize("dtype,scale,qmul,kmul", [
     ("float16", 0.6, 1.0, 1.0),     # scale log2 e = 0.87: Q pre-scaled in registers
     ("float16", 0.125, 3.0, 3.0),   # pre-scaled, scores of magnitude ~50 from larger inputs
-    ("bfloat16", 1.0, 1.0, 1.0),    # bf16: the FMA path
+    ("bfloat16", 0.125, 1.0, 1.0),  # pre-scaled
+    ("bfloat16", 0.125, 3.0, 3.0),  # pre-scaled, large scores: Q's bf16 rounding shows
+    ("bfloat16", 1.0, 1.0, 1.0),    # scale log2 e = 1.44: the FMA path
     ("float16", 2.0, 1e4, 1e-4),    # scale log2 e = 2.9: |Q| up to ~4e4 would overflow fp16 if pre-scaled
-], ids=["f16-prescaled", "f16-prescaled-large", "bf16-fma-path", "f16-fma-path"])
+], ids=["f16-prescaled", "f16-prescaled-large", "bf16-prescaled", "bf16-prescaled-large", "bf16-fma-path",
+        "f16-fma-path"])
 def test_prescaled_and_fma_exponent_paths(dtype, scale, qmul, kmul):
     """The two ways the kernel forms x = s scale log2 e - m (Q pre-scaled
     with -m as the score MFMAs' C operand, or one FMA per score), with large
-    scores that need the running-maximum raise (a late key dominates)."""
+    scores that need the running-maximum raise (a late key dominates).  The
+    pre-scaled path rounds q scale log2 e into the dtype: each exponent then
+    moves by up to eps sum_d |q_d k_d| scale log2 e, which the bound adds
+    (the FMA path computes the exponents from exact products in fp32)."""
     rng = np.random.default_rng(int(scale * 10) + (dtype == "bfloat16"))
     q = quantize((rng.standard_normal((2, 200, 64)) * qmul).astype(np.float32), dtype)
     k = rng.standard_normal((2, 320, 64)).astype(np.float32)
@@ -109,7 +116,14 @@ def test_prescaled_and_fma_exponent_paths(dtype, scale, qmul, kmul):
     o = down(g.dev_scaled_dot_product_attention(up(q, dtype), up(k, dtype), up(v, dtype), scale))
     o64 = sdpa64(q, k, v, scale)
     assert np.all(np.isfinite(o))
-    assert float(np.max(np.abs(o - o64))) <= bound(q, k, v, scale, dtype)
+    b = bound(q, k, v, scale, dtype)
+    if scale * math.log2(math.e) <= 1.0:
+        # |d x| <= eps_Q * scale log2 e * max_k sum_d |q_d k_d| moves each
+        # weight by a factor 2^dx and the output by <= (2^dx - 1) 2 max|v|
+        absdot = np.abs(q.astype(np.float64)) @ np.swapaxes(np.abs(k.astype(np.float64)), -1, -2)
+        dx = EPS[dtype] * scale * math.log2(math.e) * float(np.max(absdot))
+        b += (2.0 ** dx - 1.0) * 2 * float(np.max(np.abs(v)))
+    assert float(np.max(np.abs(o - o64))) <= b
 
 
 @pytest.mark.parametrize("shape", [(2, 40, 100, 64), (1, 64, 64, 32), (1, 33, 128, 80)],
