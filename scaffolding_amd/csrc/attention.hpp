@@ -330,15 +330,25 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
     // its exponentials before its P V MFMAs.
     constexpr bool PCHECK = std::is_same<T, F16>::value;
     const bool first = j == kb0;
+    // bf16 checks these maxima every key block: there the NaN-propagating
+    // maximum (v_maximum3_f32) runs on the MFMA results as they are, where
+    // fmaxf would first quiet possible signalling NaNs (8 fewer VALU
+    // instructions per block; a row holding a NaN score is NaN either way).
+    auto mx2 = [](float a, float b) {
+      if constexpr (PCHECK)
+        return fmaxf(a, b);
+      else
+        return __builtin_elementwise_maximum(a, b);
+    };
     auto row_max = [&](int mb) {
-      float mx = fmaxf(fmaxf(s[mb][0][0], s[mb][0][1]), s[mb][0][2]);
-      mx = fmaxf(fmaxf(mx, s[mb][0][3]), s[mb][1][0]);
-      mx = fmaxf(fmaxf(mx, s[mb][1][1]), s[mb][1][2]);
-      mx = fmaxf(fmaxf(mx, s[mb][1][3]), s[mb][2][0]);
-      mx = fmaxf(fmaxf(mx, s[mb][2][1]), s[mb][2][2]);
-      mx = fmaxf(fmaxf(mx, s[mb][2][3]), s[mb][3][0]);
-      mx = fmaxf(fmaxf(mx, s[mb][3][1]), s[mb][3][2]);
-      return fmaxf(mx, s[mb][3][3]);
+      float mx = mx2(mx2(s[mb][0][0], s[mb][0][1]), s[mb][0][2]);
+      mx = mx2(mx2(mx, s[mb][0][3]), s[mb][1][0]);
+      mx = mx2(mx2(mx, s[mb][1][1]), s[mb][1][2]);
+      mx = mx2(mx2(mx, s[mb][1][3]), s[mb][2][0]);
+      mx = mx2(mx2(mx, s[mb][2][1]), s[mb][2][2]);
+      mx = mx2(mx2(mx, s[mb][2][3]), s[mb][3][0]);
+      mx = mx2(mx2(mx, s[mb][3][1]), s[mb][3][2]);
+      return mx2(mx, s[mb][3][3]);
     };
     // Raises row block mb's reference by its row maxima (all four lanes of
     // a row), lowers x, and scales O and the row sums.
