@@ -323,17 +323,21 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
     // a split part likewise sets its own m).  Otherwise P = 2^x <=
     // 2^THRESH.
     //
-    // fp16 (PCHECK): after the first key block the check runs on the packed
-    // P instead, three values per v_pk_maximum3_f16 (4 instructions per row
-    // block instead of 8 v_max3_f32): P > 2^THRESH (as 16-bit patterns,
-    // P >= 0) sends that row block through the same raise and recomputes
-    // its exponentials before its P V MFMAs.
-    constexpr bool PCHECK = std::is_same<T, F16>::value;
+    // fp16 with the FMA (PCHECK): after the first key block the check runs
+    // on the packed P instead, three values per v_pk_maximum3_f16 (4
+    // instructions per row block instead of 8 v_max3_f32): P > 2^THRESH (as
+    // 16-bit patterns, P >= 0) sends that row block through the same raise
+    // and recomputes its exponentials before its P V MFMAs.
+    constexpr bool PCHECK = std::is_same<T, F16>::value && !PRESCALE;
     const bool first = j == kb0;
-    // bf16 checks these maxima every key block: there the NaN-propagating
-    // maximum (v_maximum3_f32) runs on the MFMA results as they are, where
-    // fmaxf would first quiet possible signalling NaNs (8 fewer VALU
-    // instructions per block; a row holding a NaN score is NaN either way).
+    // Otherwise (bf16, and fp16 with PRESCALE) the maxima are checked every
+    // key block, with the NaN-propagating maximum (v_maximum3_f32) on the
+    // MFMA results as they are, where fmaxf would first quiet possible
+    // signalling NaNs (8 fewer VALU instructions per block; a row holding a
+    // NaN score is NaN either way).  For fp16 with PRESCALE this measured
+    // faster than the packed check, which costs a branch per row block (C4
+    // -3.7 %, packed 30-head C5 -1.7 %, A/B in one run); with the FMA the
+    // packed check stays ahead (+1.8 % without it).
     auto mx2 = [](float a, float b) {
       if constexpr (PCHECK)
         return fmaxf(a, b);
