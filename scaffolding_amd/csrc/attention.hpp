@@ -427,9 +427,10 @@ __global__ __launch_bounds__(256, 2) void attn64_kernel(AttnParams p) {
 #pragma unroll
       for (int db = 0; db < 4; ++db) o[MB][db] = Mfma16<T>::run(vf[db][1], pf[MB][1], o[MB][db]);
     };
-    // fp16 after the first key block: row block mb's packed P against
-    // 2^THRESH (0x5C00 = 256 in fp16; inf and NaN patterns exceed it); a
-    // row block that exceeds it is raised and its exponentials recomputed.
+    // fp16 with the FMA, after the first key block: row block mb's packed
+    // P against 2^THRESH (0x5C00 = 256 in fp16; inf and NaN patterns exceed
+    // it); a row block that exceeds it is raised and its exponentials
+    // recomputed.
     auto pcheck = [&](auto mb_c) {
       constexpr int R = decltype(mb_c)::value;
       if constexpr (PCHECK) {
