@@ -651,23 +651,68 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
   uint16_t* C = static_cast<uint16_t*>(p.C) + b * p.sC;
   const bool vec_ok = ((p.ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
   // Residual: read in the accumulator layout (4 consecutive columns of one
-  // row per lane) and added before the single rounding.  R may be C: every
-  // element of R is read in a pass before that pass stores it.
-  const void* R = p.res != nullptr ? static_cast<const uint16_t*>(p.res) + b * p.sR : nullptr;
+  // row per lane, as raw 16-bit pairs) and added before the single
+  // rounding.  With a K-contiguous B (the forward products, where the
+  // residual is used) each pass's residual is loaded one pass ahead, the
+  // first pass's before the epilogue's first barrier, so only that one
+  // load's latency is exposed per tile instead of one per pass (R may alias
+  // C, which keeps the compiler from hoisting them itself; measured on
+  // 17776 x 1920 x 1920 bf16: the residual cost 22 us of 146 loaded in
+  // each pass).  With a k-major B the registers are not there, and each
+  // pass loads its own.  R may be C: the passes cover disjoint rows, so
+  // every element of R is still read before the pass that stores it.
+  const uint16_t* R = p.res != nullptr ? static_cast<const uint16_t*>(p.res) + b * p.sR : nullptr;
   const bool rvec = R != nullptr && res_vec_ok<TOut>(R, p.ldr);
+  constexpr int NPASS = WM / ROWS_S;
+  constexpr int RB = ROWS_S / 16;  // row blocks per pass
+  constexpr bool RES_AHEAD = B_KM;
+  // Rows past M read row M - 1 (their sums are not stored), columns past N
+  // read as zero.
+  auto rload = [&](int ps, u32x2 (&rw)[RB][FN]) {
+#pragma unroll
+    for (int jj = 0; jj < RB; ++jj) {
+      const int gm = m0 + wm * WM + (ps * RB + jj) * 16 + (elane & 15);
+      const uint16_t* rrow = R + (int64_t)(gm < M ? gm : M - 1) * p.ldr;
+#pragma unroll
+      for (int i = 0; i < FN; ++i) {
+        const int n = n0 + wn * WN + i * 16 + 4 * (elane >> 4);
+        if (rvec && n + 3 < N) {
+          rw[jj][i] = *reinterpret_cast<const u32x2*>(rrow + n);
+        } else {
+          uint32_t h[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) h[q] = n + q < N ? rrow[n + q] : 0u;
+          rw[jj][i] = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+        }
+      }
+    }
+  };
   // MASKED: a part of a shared split sum, which stores only its own row
   // blocks; whole tiles compile without that test.
   auto epilogue = [&](auto masked_c) {
   constexpr bool MASKED = decltype(masked_c)::value;
   with_act(act, [&](auto act_c) {
   constexpr int ACT = decltype(act_c)::value;
+  u32x2 rcur[RB][FN];
+  if constexpr (RES_AHEAD)
+    if (R != nullptr) rload(0, rcur);
 #pragma unroll
-  for (int ps = 0; ps < WM / ROWS_S; ++ps) {
+  for (int ps = 0; ps < NPASS; ++ps) {
+    u32x2 rnext[RB][FN];
+    if constexpr (RES_AHEAD)
+      if (R != nullptr && ps + 1 < NPASS) rload(ps + 1, rnext);
     // A part of a shared split sum skips passes without a row block of its
     // own (workgroup-uniform); a workgroup barrier has already followed the
     // main loop there.
     if constexpr (MASKED)
-      if (((own >> (ps * (ROWS_S / 16))) & ((1 << (ROWS_S / 16)) - 1)) == 0) continue;
+      if (((own >> (ps * (ROWS_S / 16))) & ((1 << (ROWS_S / 16)) - 1)) == 0) {
+        if constexpr (RES_AHEAD)
+#pragma unroll
+          for (int jj = 0; jj < RB; ++jj)
+#pragma unroll
+            for (int i = 0; i < FN; ++i) rcur[jj][i] = rnext[jj][i];
+        continue;
+      }
     // The staging region is private to this wave: only the first pass
     // waits for the other waves (their last fragment reads of the main loop
     // may touch it); later passes order this wave's own LDS accesses.
@@ -685,12 +730,19 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[q] = act_t<ACT>(acc[i][j][q] * alpha + bv[i][q]);
         if (R != nullptr) {
-          const int gm = m0 + wm * WM + j * 16 + (elane & 15);
-          if (gm < M) {
-            float rr[4];
-            Res4<TOut>::load(R, (int64_t)gm * p.ldr, n0 + wn * WN + i * 16 + 4 * (elane >> 4), N, rvec, rr);
+          if constexpr (RES_AHEAD) {
+            const u32x2 rw = rcur[jj][i];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) v[q] += rr[q];
+            for (int q = 0; q < 4; ++q)
+              v[q] += Elem<TOut>::to_f32(static_cast<uint16_t>(rw[q >> 1] >> ((q & 1) * 16)));
+          } else {
+            const int gm = m0 + wm * WM + j * 16 + (elane & 15);
+            if (gm < M) {
+              float rr[4];
+              Res4<TOut>::load(R, (int64_t)gm * p.ldr, n0 + wn * WN + i * 16 + 4 * (elane >> 4), N, rvec, rr);
+#pragma unroll
+              for (int q = 0; q < 4; ++q) v[q] += rr[q];
+            }
           }
         }
         const uint32_t lo = pack2<TOut>(v[0], v[1]);
@@ -725,6 +777,11 @@ __global__ __launch_bounds__(512) void gemm16nt_pp_kernel(GemmParams p) {
         }
       }
     }
+    if constexpr (RES_AHEAD)
+#pragma unroll
+      for (int jj = 0; jj < RB; ++jj)
+#pragma unroll
+        for (int i = 0; i < FN; ++i) rcur[jj][i] = rnext[jj][i];
   }
   });
   };

@@ -207,6 +207,50 @@ def test_gemm_add_in_place_and_batched():
     check_bound(down(out), y64, gemm_bound(y64, absprod, k, "float16"), "batched broadcast residual")
 
 
+@pytest.mark.parametrize("case", [
+    ("bfloat16", 4096, 4096, 128, "gemm nt 256x256 lds-dma"),
+    ("bfloat16", 4352, 4096, 4096, "gemm nt 256x256 lds-dma 16-bit persistent split"),
+    ("float16", 4352, 7936, 256, "gemm nt 256x256 lds-dma 16-bit persistent"),
+    ("bfloat16", 17776, 1920, 1920, "gemm nt 256x256 lds-dma 16-bit persistent split"),
+], ids=lambda c: "%s-%dx%dx%d" % c[:4])
+def test_gemm_add_in_place_bitwise_8wave(case):
+    """The 8-wave kernel loads each epilogue pass's residual one pass ahead
+    of its stores: with R == C (the residual accumulated in place) every
+    element must still be read before it is overwritten, so the in-place
+    result equals the out-of-place one bit for bit, whole tiles, persistent
+    tiles and the split tail's shared final sum (parts storing only their
+    own rows) alike.  Ragged M and N edges included (17776 rows, N = 7936)."""
+    dtype, m, n, k, kern = case
+    so = _lib()
+    g = cu()
+    rng = np.random.default_rng(m + n + k)
+    x = rnd(rng, (m, k), 1.0, dtype)
+    w = rnd(rng, (n, k), 1.0 / np.sqrt(k), dtype)
+    bias = rnd(rng, (n,), 0.5, dtype)
+    r = rnd(rng, (m, n), 1.0, dtype)
+    gx, gw, gbias = up(x, dtype), up(w, dtype), up(bias, dtype)
+    plan = g.gemm_plan(1, m, n, k, 1, gx.data_ptr, k, 0, gw.data_ptr, k, 0, n, m * n, dtype, epi=1, ptr_bias=16)
+    assert plan.startswith(kern), plan
+    dt = 1 if dtype == "float16" else 2
+    P, I64 = ctypes.c_void_p, ctypes.c_int64
+    outs = []
+    for in_place in (False, True):
+        gr = up(r, dtype)
+        gc = gr if in_place else g.empty((m, n), gr.dtype)
+        rc = so.sf_gemm_add(0, 1, I64(m), I64(n), I64(k), I64(1), P(gx.data_ptr), I64(k), I64(0),
+                            P(gw.data_ptr), I64(k), I64(0), P(gc.data_ptr), I64(n), I64(0), dt, dt,
+                            ctypes.c_float(1.0), P(gbias.data_ptr), 1, P(gr.data_ptr), I64(n), I64(0), None)
+        assert rc == 0, so.sf_last_error()
+        outs.append(g.gputensor_bits_to_numpy(gc))
+    assert np.array_equal(outs[0], outs[1])
+    # sampled rows (both ends, the ragged last tile) against fp64
+    rows = np.unique(np.r_[0, m - 1, m - 2, np.arange(0, m, 997), np.arange(max(0, m - 300), m, 37)])
+    y = down(g.dev_linear_forward(gx, gw, gbias, None, up(r, dtype)))[rows]
+    y64 = ref.linear_f64(x[rows], w, bias) + r[rows].astype(np.float64)
+    absprod = np.abs(x[rows].astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+    check_bound(y, y64, gemm_bound(y64, absprod, k, dtype), "residual in place %s" % (case,))
+
+
 # ------------------------------------------------------------------ attention over packed heads
 
 def attn_bound(v, dtype, sk):
