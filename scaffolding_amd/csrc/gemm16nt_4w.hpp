@@ -304,8 +304,35 @@ __global__ __launch_bounds__(256, 1) void gemm16nt_4w_kernel(GemmParams p) {
   constexpr int ROWS_I = 64 / LANES_ROW;  // 4 rows per store instruction
   uint16_t* C = static_cast<uint16_t*>(p.C) + b * p.sC;
   const bool vec_ok = ((p.ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
-  const void* R = p.res != nullptr ? static_cast<const uint16_t*>(p.res) + b * p.sR : nullptr;
+  // Residual: the wave's whole 128 x 128 block of R is loaded before the
+  // epilogue's first barrier (raw 16-bit pairs in the accumulator layout,
+  // 128 registers that the main loop's fragments have freed), so its
+  // latency is paid once per tile, not once per pass (R may alias C, which
+  // keeps the compiler from hoisting the loads itself).  R may be C: every
+  // element is read here, before any store.  Rows past M read row M - 1
+  // (not stored), columns past N read as zero.
+  const uint16_t* R = p.res != nullptr ? static_cast<const uint16_t*>(p.res) + b * p.sR : nullptr;
   const bool rvec = R != nullptr && res_vec_ok<TOut>(R, p.ldr);
+  u32x2 rall[WM / 16][FN];
+  if (R != nullptr) {
+#pragma unroll
+    for (int j = 0; j < WM / 16; ++j) {
+      const int gm = m0 + wm * WM + j * 16 + (elane & 15);
+      const uint16_t* rrow = R + (int64_t)(gm < M ? gm : M - 1) * p.ldr;
+#pragma unroll
+      for (int i = 0; i < FN; ++i) {
+        const int n = n0 + wn * WN + i * 16 + 4 * (elane >> 4);
+        if (rvec && n + 3 < N) {
+          rall[j][i] = *reinterpret_cast<const u32x2*>(rrow + n);
+        } else {
+          uint32_t h[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) h[q] = n + q < N ? rrow[n + q] : 0u;
+          rall[j][i] = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+        }
+      }
+    }
+  }
   {
 #pragma unroll
     for (int ps = 0; ps < WM / ROWS_S; ++ps) {
@@ -325,13 +352,10 @@ __global__ __launch_bounds__(256, 1) void gemm16nt_4w_kernel(GemmParams p) {
 #pragma unroll
           for (int q = 0; q < 4; ++q) v[q] = act_t<ACT>(acc_read(acc[i][j][q]) * alpha + bv[i][q]);
           if (R != nullptr) {
-            const int gm = m0 + wm * WM + j * 16 + (elane & 15);
-            if (gm < M) {
-              float rr[4];
-              Res4<TOut>::load(R, (int64_t)gm * p.ldr, n0 + wn * WN + i * 16 + 4 * (elane >> 4), N, rvec, rr);
+            const u32x2 rw = rall[j][i];
 #pragma unroll
-              for (int q = 0; q < 4; ++q) v[q] += rr[q];
-            }
+            for (int q = 0; q < 4; ++q)
+              v[q] += Elem<TOut>::to_f32(static_cast<uint16_t>(rw[q >> 1] >> ((q & 1) * 16)));
           }
           const uint32_t lo = pack2<TOut>(v[0], v[1]);
           const uint32_t hi = pack2<TOut>(v[2], v[3]);
